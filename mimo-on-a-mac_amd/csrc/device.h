@@ -1,0 +1,193 @@
+// Device helpers shared by the MoE kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mimo {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// round-to-nearest-even float -> bf16 bits; NaN stays a quiet NaN
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ------------------------------------------------------------------ E2M1 / E8M0
+// E2M1 magnitude code for y >= 0 already divided by the block scale: nearest-even on
+// {0, .5, 1, 1.5, 2, 3, 4, 6}, saturating at 6 (OCP MX v1.0).
+__device__ __forceinline__ uint32_t e2m1_mag_code(float y) {
+  float v;
+  if (y < 2.0f) v = rintf(y * 2.0f) * 0.5f;
+  else if (y < 4.0f) v = rintf(y);
+  else v = rintf(y * 0.5f) * 2.0f;
+  // v in {0,.5,1,1.5,2,3,4,6,8}
+  if (v >= 6.0f) return 7u;
+  if (v >= 4.0f) return 6u;
+  if (v >= 3.0f) return 5u;
+  if (v >= 2.0f) return 4u;
+  return (uint32_t)(v * 2.0f);  // 0, 1, 2, 3
+}
+
+// ------------------------------------------------------------------ E4M3 (activation hi/lo split)
+// magnitude code for 0 <= y <= 448 (y exactly representable scaling of a bf16 value), nearest-even.
+__device__ __forceinline__ uint32_t e4m3_mag_code(float y) {
+  if (y < 0.015625f) {                       // below 2^-6: subnormal, quantum 2^-9
+    return (uint32_t)rintf(y * 512.0f);      // 8 == smallest normal, same encoding
+  }
+  uint32_t u = __float_as_uint(y);
+  int e = (int)((u >> 23) & 0xFF) - 127;
+  uint32_t f = u & 0x7FFFFFu;
+  uint32_t q = f >> 20, rem = f & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ++q;
+  if (q == 8u) { q = 0; ++e; }
+  uint32_t code = ((uint32_t)(e + 7) << 3) | q;
+  return code > 0x7Eu ? 0x7Eu : code;
+}
+__device__ __forceinline__ float e4m3_decode_mag(uint32_t c) {
+  uint32_t e = (c >> 3) & 0xF, m = c & 7;
+  return e == 0 ? (float)m * 0.001953125f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+}
+// E8M0 exponent X for an E4M3 block with maximum magnitude amax: amax / 2^X in (224, 448].
+__device__ __forceinline__ int fp8_block_exp(float amax) {
+  if (amax == 0.0f) return 0;
+  uint32_t u = __float_as_uint(amax);
+  int E = (int)((u >> 23) & 0xFF);
+  int e = E == 0 ? -127 : E - 127;
+  int X = (u & 0x7FFFFFu) > 0x600000u ? e - 7 : e - 8;
+  return X < -127 ? -127 : (X > 127 ? 127 : X);
+}
+__device__ __forceinline__ float exp2i(int X) {   // 2^X for -127 <= X <= 127, exact
+  return X >= -126 ? __uint_as_float((uint32_t)(X + 127) << 23) : __uint_as_float(0x00400000u);
+}
+// Signed E4M3 code of v / 2^X (positive zero for a zero magnitude); returns code, writes decoded value.
+__device__ __forceinline__ uint32_t e4m3_encode(float v, int X, float* dec) {
+  float inv = exp2i(-X);        // exact when -X in range; X >= -127 so -X <= 127
+  float y = fabsf(v) * inv;
+  uint32_t mag = e4m3_mag_code(y);
+  float dv = e4m3_decode_mag(mag) * exp2i(X);
+  uint32_t sgn = (mag != 0u && v < 0.0f) ? 0x80u : 0u;
+  *dec = sgn ? -dv : dv;
+  return mag | sgn;
+}
+
+// ------------------------------------------------------------------ the specified sigmoid
+// exp(x) for |x| <= 200: Cody-Waite reduction by ln 2 (fdlibm split) and a degree-13 Taylor polynomial in
+// Horner form, every step one correctly rounded IEEE double operation (no contraction), so the result is
+// reproducible bit for bit on any IEEE platform that evaluates the same sequence.
+__device__ __forceinline__ double exp_spec(double x) {
+#pragma clang fp contract(off)
+  const double LN2_HI = 0x1.62e42feep-1;
+  const double LN2_LO = 0x1.a39ef35793c76p-33;
+  const double INV_LN2 = 0x1.71547652b82fep+0;
+  double n = __builtin_rint(x * INV_LN2);
+  double r = (x - n * LN2_HI) - n * LN2_LO;
+  double p = 1.0 / 6227020800.0;             // 1/13!
+  p = p * r + 1.0 / 479001600.0;             // 1/12!
+  p = p * r + 1.0 / 39916800.0;
+  p = p * r + 1.0 / 3628800.0;
+  p = p * r + 1.0 / 362880.0;
+  p = p * r + 1.0 / 40320.0;
+  p = p * r + 1.0 / 5040.0;
+  p = p * r + 1.0 / 720.0;
+  p = p * r + 1.0 / 120.0;
+  p = p * r + 1.0 / 24.0;
+  p = p * r + 1.0 / 6.0;
+  p = p * r + 0.5;
+  p = p * r + 1.0;
+  p = p * r + 1.0;
+  return __builtin_ldexp(p, (int)n);
+}
+// fp32 sigmoid = fp32(1 / (1 + exp_spec(-x))), input clamped to [-200, 200]; NaN -> canonical quiet NaN.
+__device__ __forceinline__ float sigmoid_spec(float xf) {
+#pragma clang fp contract(off)
+  if (xf != xf) return __uint_as_float(0x7FC00000u);
+  double x = (double)xf;
+  if (x < -200.0) x = -200.0;
+  if (x > 200.0) x = 200.0;
+  double e = exp_spec(-x);
+  return (float)(1.0 / (1.0 + e));
+}
+
+// 32 bf16-valued floats -> hi / lo E4M3 words (4 codes per word, element order) and E8M0 bytes:
+// hi = E4M3 block quantisation of v, lo = the same of the exact residual v - hi.
+__device__ __forceinline__ void quant_block_fp8_hilo(const float* v, uint32_t* hw, uint32_t* lw, uint8_t* hsb,
+                                                     uint8_t* lsb) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  int X = fp8_block_exp(amax);
+  float r[32];
+  float ramax = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float dec;
+      uint32_t c = e4m3_encode(v[w * 4 + j], X, &dec);
+      word |= c << (8 * j);
+      r[w * 4 + j] = v[w * 4 + j] - dec;
+      ramax = fmaxf(ramax, fabsf(r[w * 4 + j]));
+    }
+    hw[w] = word;
+  }
+  int Y = fp8_block_exp(ramax);
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float dec;
+      word |= e4m3_encode(r[w * 4 + j], Y, &dec) << (8 * j);
+    }
+    lw[w] = word;
+  }
+  *hsb = (uint8_t)(X + 127);
+  *lsb = (uint8_t)(Y + 127);
+}
+
+// ------------------------------------------------------------------ wave reductions (wave64)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor(v, o, 64);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+// max over groups of `width` consecutive lanes (width a power of two <= 64)
+__device__ __forceinline__ float group_max(float v, int width) {
+  for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// order-preserving map of an fp32 key to uint32 (NaN lowest, -0 treated as +0)
+__device__ __forceinline__ uint32_t key_to_ordered(float k) {
+  if (k != k) return 0u;
+  if (k == 0.0f) k = 0.0f;
+  uint32_t u = __float_as_uint(k);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ------------------------------------------------------------------ misc
+__device__ __forceinline__ uint32_t load_u8x4(const uint8_t* p) { return *(const uint32_t*)p; }
+
+}  // namespace mimo

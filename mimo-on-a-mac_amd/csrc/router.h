@@ -1,0 +1,40 @@
+// Launchers shared between the router, decode and prefill translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mimo {
+
+struct RouterSmallArgs {
+  const uint16_t* x;       // [T, H] bf16
+  const uint16_t* Wg;      // [E, H] bf16
+  const float* bias;       // [E]
+  int T, H, E, k, nlog;    // nlog = ceil(E / 4) logits blocks
+  float* logits;           // [T, E]
+  float* scores;           // [T, E] sigmoid
+  float* keys;             // [T, E] sigmoid + bias
+  int* counter;            // last-block-done counter (zero between launches)
+  int32_t* inds_out;       // [T, k] optional
+  float* w_out;            // [T, k] optional
+  uint8_t *xq_hi, *xq_lo, *xq_hs, *xq_ls;   // optional fp8 split of x: [T, H], [T, H/32]
+  // optional grouping (uids == nullptr: skip)
+  const int32_t* slot_of;
+  int R, n_slots, Umax;
+  int32_t *uids, *urows, *ucnt;
+  float* uw;
+  uint32_t* gidx;
+  int32_t *n_unique, *status;
+};
+
+int launch_router_small(const RouterSmallArgs& a, hipStream_t st);
+int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st);
+int launch_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling, int32_t* inds,
+                         float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
+                         hipStream_t st);
+int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
+                    int32_t* inv, int tile_rows, int32_t* tile_off, int32_t* status, hipStream_t st);
+size_t dispatch_workspace(int n, int n_slots);
+int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint8_t* hi, uint8_t* hs, uint8_t* lo,
+                             uint8_t* ls, hipStream_t st);
+
+}  // namespace mimo

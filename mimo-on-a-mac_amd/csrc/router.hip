@@ -1,0 +1,496 @@
+// Router (gate linear, sigmoid + bias selection, top-k, renormalisation), distinct-expert grouping and the
+// prefill counting-sort dispatch.
+//
+// Reference: Router.__call__ engine/mimo_stream/model.py:58-65; group_routes engine/mimo_stream/kernels.py:
+// 149-173; prefill dispatch model.py:235-242, :266-268.  Selection order is canonical: descending key
+// (sigmoid + bias), ties to the lower expert id, NaN keys last; weights are renormalised with a sequential
+// fp32 sum in that order.  Everything here is integer or exactly specified fp32/fp64 arithmetic, so routes
+// and permutations are bit-exact against the oracle given identical logits.
+#include "device.h"
+#include "host.h"
+#include "router.h"
+
+namespace mimo {
+
+// ------------------------------------------------------------------ selection (one wave per row)
+// keys/scores for row r live in s_row/key_row (global or LDS); writes k (index, weight) pairs.
+__device__ void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,
+                                int32_t* inds_out, float* w_out, int* lds_sel) {
+  const int lane = threadIdx.x & 63;
+  // candidates of this lane: e = lane + 64 * j
+  uint64_t cand[16];
+  const int per = (E + 63) / 64;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int e = lane + 64 * j;
+    cand[j] = 0;
+    if (j < per && e < E) cand[j] = ((uint64_t)key_to_ordered(key_row[e]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+    // a NaN key maps to 0 in the high word; the low word (> 0) keeps it selectable, ordered by id
+  }
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = 0;
+    int bj = -1;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (cand[j] > best) { best = cand[j]; bj = j; }
+    uint64_t wbest = wave_max_u64(best);
+    if (best == wbest) {                          // exactly one lane owns the maximum (ids are unique)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (j == bj) cand[j] = 0;
+    }
+    if (lane == 0) lds_sel[r] = (int)(0xFFFFFFFFu - (uint32_t)(wbest & 0xFFFFFFFFu));
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+    for (int r = 0; r < k; ++r) acc = acc + s_row[lds_sel[r]];
+    float denom = acc + 1e-20f;
+    for (int r = 0; r < k; ++r) {
+      float wv = s_row[lds_sel[r]] / denom;
+      if (scaling != 1.0f) wv = wv * scaling;
+      inds_out[r] = lds_sel[r];
+      w_out[r] = wv;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// ------------------------------------------------------------------ grouping (one block, <= 1024 routes)
+// group_routes restated: uids ascending, urows/uw in route order per expert, gidx = u*R + c.
+// Requires blockDim.x >= n_routes and LDS `present` of n_slots ints.
+__device__ void block_group_routes(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k,
+                                   int R, int n_slots, int Umax, int32_t* uids, int32_t* urows, int32_t* ucnt,
+                                   float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status, int* present,
+                                   int* route_slot) {
+  const int tid = threadIdx.x;
+  const int nr = M * k;
+  for (int i = tid; i < n_slots; i += blockDim.x) present[i] = 0;
+  for (int i = tid; i < Umax * R; i += blockDim.x) { urows[i] = 0; uw[i] = 0.0f; }
+  for (int i = tid; i < Umax; i += blockDim.x) { ucnt[i] = 0; uids[i] = 0; }
+  __syncthreads();
+  int bad = 0;
+  if (tid < nr) {
+    int e = inds[tid];
+    int s = slot_of ? (e >= 0 ? slot_of[e] : -1) : e;
+    if (s < 0 || s >= n_slots) { bad = MIMO_ERR_SLOT; s = 0; }
+    route_slot[tid] = s;
+    present[s] = 1;
+  }
+  __syncthreads();
+  if (tid == 0) {          // ascending ranks of present slots (sequential, deterministic)
+    int u = 0;
+    for (int s = 0; s < n_slots; ++s) {
+      if (present[s]) { present[s] = u + 1; ++u; }
+    }
+    n_unique[0] = u;
+  }
+  __syncthreads();
+  if (tid < nr) {
+    int s = route_slot[tid];
+    int u = present[s] - 1;
+    int c = 0;
+    for (int t = 0; t < tid; ++t) c += (route_slot[t] == s);
+    if (c >= R) {
+      bad = MIMO_ERR_ROWS_PER_EXPERT;
+    } else if (u < Umax) {
+      urows[u * R + c] = tid / k;
+      uw[u * R + c] = scores[tid];
+      gidx[tid] = (uint32_t)(u * R + c);
+      uids[u] = s;
+      int total = c;
+      for (int t = tid + 1; t < nr; ++t) total += (route_slot[t] == s);
+      if (c == 0) ucnt[u] = total + 1 > R ? R : total + 1;
+    }
+  }
+  // status: first nonzero code wins deterministically (lowest route index)
+  __shared__ int s_bad;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  if (bad) atomicMin(&s_bad, bad);      // codes are negative: min = most severe, order independent
+  __syncthreads();
+  if (tid == 0) status[0] = s_bad;
+}
+
+// ------------------------------------------------------------------ small-T router (T <= 8)
+// Blocks [0, nlog): one wave per expert computes T logits (fp32 FMA over bf16 products), its sigmoid and key.
+// Blocks [nlog, nlog + nquant): fp8 hi/lo split of x (one thread per 32-block) for the expert kernels.
+// The last logits block to finish selects top-k per row (one wave per row) and, if grouping is requested,
+// groups routes by distinct slot.  The done-counter is left at zero.
+__global__ void __launch_bounds__(256) router_small_kernel(RouterSmallArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if ((int)blockIdx.x >= a.nlog) {
+    if (!a.xq_hi) return;
+    int64_t b = (int64_t)(blockIdx.x - a.nlog) * blockDim.x + threadIdx.x;
+    int64_t nb = (int64_t)a.T * (a.H / 32);
+    if (b >= nb) return;
+    const uint4* src = reinterpret_cast<const uint4*>(a.x + b * 32);
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint4 d = src[c];
+      uint32_t parts[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[c * 8 + 2 * j] = __uint_as_float(parts[j] << 16);
+        v[c * 8 + 2 * j + 1] = __uint_as_float(parts[j] & 0xFFFF0000u);
+      }
+    }
+    uint32_t hw[8], lw[8];
+    uint8_t hsb, lsb;
+    quant_block_fp8_hilo(v, hw, lw, &hsb, &lsb);
+    uint4* Hp = reinterpret_cast<uint4*>(a.xq_hi + b * 32);
+    uint4* Lp = reinterpret_cast<uint4*>(a.xq_lo + b * 32);
+    Hp[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    Hp[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    Lp[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    Lp[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    a.xq_hs[b] = hsb;
+    a.xq_ls[b] = lsb;
+    return;
+  }
+  const int e = blockIdx.x * 4 + wave;
+  if (e < a.E) {
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+    const uint16_t* wrow = a.Wg + (size_t)e * a.H;
+    for (int k0 = lane * 8; k0 < a.H; k0 += 512) {
+      uint4 wq = *reinterpret_cast<const uint4*>(wrow + k0);
+      float wf[8];
+      uint32_t wp[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { wf[2 * j] = __uint_as_float(wp[j] << 16); wf[2 * j + 1] = __uint_as_float(wp[j] & 0xFFFF0000u); }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        if (r < a.T) {
+          uint4 xq = *reinterpret_cast<const uint4*>(a.x + (size_t)r * a.H + k0);
+          uint32_t xp[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[r] = fmaf(__uint_as_float(xp[j] << 16), wf[2 * j], acc[r]);
+            acc[r] = fmaf(__uint_as_float(xp[j] & 0xFFFF0000u), wf[2 * j + 1], acc[r]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r < a.T) {
+        float l = wave_sum(acc[r]);
+        if (lane == 0) {
+          float s = sigmoid_spec(l);
+          a.logits[r * a.E + e] = l;
+          a.scores[r * a.E + e] = s;
+          a.keys[r * a.E + e] = s + a.bias[e];
+        }
+      }
+    }
+  }
+  // last-block-done
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int old = atomicAdd(a.counter, 1);
+    s_last = (old == a.nlog - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  __shared__ int sel[4][16];
+  __shared__ int32_t s_inds[64];
+  __shared__ float s_w[64];
+  for (int r = wave; r < a.T; r += 4) {
+    wave_select_row(a.scores + r * a.E, a.keys + r * a.E, a.E, a.k, 1.0f, s_inds + r * a.k, s_w + r * a.k, sel[wave]);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.T * a.k; i += blockDim.x) {
+    if (a.inds_out) a.inds_out[i] = s_inds[i];
+    if (a.w_out) a.w_out[i] = s_w[i];
+  }
+  if (a.uids) {
+    __shared__ int present[1024];
+    __shared__ int route_slot[64];
+    block_group_routes(s_inds, s_w, a.slot_of, a.T, a.k, a.R, a.n_slots, a.Umax, a.uids, a.urows, a.ucnt, a.uw,
+                       a.gidx, a.n_unique, a.status, present, route_slot);
+  }
+  if (threadIdx.x == 0) atomicExch(a.counter, 0);
+}
+
+// ------------------------------------------------------------------ general-T logits: tiled fp32 GEMM
+// logits[t, e] = sum_h x[t, h] * W[e, h]; block tile 32 tokens x 64 experts, K chunks of 64 through LDS.
+__global__ void __launch_bounds__(256) router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ W,
+                                                            int T, int H, int E, float* __restrict__ logits) {
+  __shared__ float xs[32][65];
+  __shared__ float ws[64][65];
+  const int t0 = blockIdx.y * 32, e0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;   // 16 x 16 threads; each 2 tokens x 4 experts
+  float acc[2][4] = {};
+  for (int k0 = 0; k0 < H; k0 += 64) {
+    for (int i = threadIdx.x; i < 32 * 64; i += 256) {
+      int r = i >> 6, c = i & 63;
+      int t = t0 + r;
+      xs[r][c] = t < T ? bf16_to_f32(x[(size_t)t * H + k0 + c]) : 0.0f;
+    }
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+      int r = i >> 6, c = i & 63;
+      int e = e0 + r;
+      ws[r][c] = e < E ? bf16_to_f32(W[(size_t)e * H + k0 + c]) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int c = 0; c < 64; ++c) {
+      float xv0 = xs[ty * 2][c], xv1 = xs[ty * 2 + 1][c];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float wv = ws[tx * 4 + j][c];
+        acc[0][j] = fmaf(xv0, wv, acc[0][j]);
+        acc[1][j] = fmaf(xv1, wv, acc[1][j]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int t = t0 + ty * 2 + i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int e = e0 + tx * 4 + j;
+      if (t < T && e < E) logits[(size_t)t * E + e] = acc[i][j];
+    }
+  }
+}
+
+// one wave per row: sigmoid, key, top-k, renormalise; optional expert -> slot mapping for the dispatch
+__global__ void __launch_bounds__(256) router_select_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                            int T, int E, int k, float scaling, int32_t* inds,
+                                                            float* w, const int32_t* slot_of, int32_t* slot_inds,
+                                                            int n_slots, int32_t* status) {
+  extern __shared__ float sm[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* s_row = sm + wave * 2 * E;
+  float* k_row = s_row + E;
+  __shared__ int sel[4][16];
+  __shared__ int32_t oi[4][16];
+  __shared__ float ow[4][16];
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  for (int e = lane; e < E; e += 64) {
+    float s = sigmoid_spec(logits[(size_t)t * E + e]);
+    s_row[e] = s;
+    k_row[e] = s + bias[e];
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  wave_select_row(s_row, k_row, E, k, scaling, oi[wave], ow[wave], sel[wave]);
+  if (lane < k) {
+    int e = oi[wave][lane];
+    if (inds) inds[(size_t)t * k + lane] = e;
+    if (w) w[(size_t)t * k + lane] = ow[wave][lane];
+    if (slot_inds) {
+      int s = slot_of ? slot_of[e] : e;
+      if (s < 0 || s >= n_slots) { atomicMin(status, MIMO_ERR_SLOT); s = 0; }
+      slot_inds[(size_t)t * k + lane] = s;
+    }
+  }
+}
+
+__global__ void group_routes_kernel(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k,
+                                    int R, int n_slots, int Umax, int32_t* uids, int32_t* urows, int32_t* ucnt,
+                                    float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status) {
+  __shared__ int present[1024];
+  __shared__ int route_slot[1024];
+  block_group_routes(inds, scores, slot_of, M, k, R, n_slots, Umax, uids, urows, ucnt, uw, gidx, n_unique, status,
+                     present, route_slot);
+}
+
+// ------------------------------------------------------------------ prefill dispatch (stable counting sort)
+constexpr int DISPATCH_CHUNK = 1024;
+
+// slot ids outside [0, n_slots) are counted as slot 0 and flagged in *status (never indexed out of bounds)
+__device__ __forceinline__ int checked_slot(const int32_t* slots, int i, int n_slots, int32_t* status) {
+  int s = slots[i];
+  if (s < 0 || s >= n_slots) {
+    if (status) atomicMin(status, MIMO_ERR_SLOT);
+    s = 0;
+  }
+  return s;
+}
+
+__global__ void __launch_bounds__(1024) dispatch_hist_kernel(const int32_t* __restrict__ slots, int n, int n_slots,
+                                                             int32_t* __restrict__ hist, int32_t* status) {
+  extern __shared__ int h[];
+  for (int i = threadIdx.x; i < n_slots; i += blockDim.x) h[i] = 0;
+  __syncthreads();
+  int i = blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
+  if (i < n) atomicAdd(&h[checked_slot(slots, i, n_slots, status)], 1);   // integer counts: order independent
+  __syncthreads();
+  for (int s = threadIdx.x; s < n_slots; s += blockDim.x) hist[(size_t)blockIdx.x * n_slots + s] = h[s];
+}
+
+// offsets[s] = exclusive scan of per-slot totals; base[b][s] = offsets[s] + sum_{b' < b} hist[b'][s];
+// tile_off[s] = exclusive scan of ceil(count[s] / tile_rows) (row tiles of the grouped GEMM).
+__global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int n_slots,
+                                                             int32_t* __restrict__ offsets, int tile_rows,
+                                                             int32_t* __restrict__ tile_off) {
+  extern __shared__ int sh[];
+  int* tot = sh;
+  int* til = sh + n_slots;
+  for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
+    int acc = 0;
+    for (int b = 0; b < nchunks; ++b) acc += hist[(size_t)b * n_slots + s];
+    tot[s] = acc;
+    til[s] = tile_rows > 0 ? (acc + tile_rows - 1) / tile_rows : 0;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0, trun = 0;
+    for (int s = 0; s < n_slots; ++s) {
+      int c = tot[s], tc = til[s];
+      tot[s] = run;
+      til[s] = trun;
+      run += c;
+      trun += tc;
+    }
+    offsets[n_slots] = run;
+    if (tile_off) tile_off[n_slots] = trun;
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
+    offsets[s] = tot[s];
+    if (tile_off) tile_off[s] = til[s];
+    int acc = tot[s];
+    for (int b = 0; b < nchunks; ++b) {
+      int c = hist[(size_t)b * n_slots + s];
+      hist[(size_t)b * n_slots + s] = acc;
+      acc += c;
+    }
+  }
+}
+
+// stable placement: rank within the chunk = (earlier waves' count of the slot) + (earlier lanes of the wave)
+__global__ void __launch_bounds__(1024) dispatch_place_kernel(const int32_t* __restrict__ slots, int n, int n_slots,
+                                                              const int32_t* __restrict__ base,
+                                                              int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+  // slot ids were range-checked (and flagged) by dispatch_hist_kernel; clamp identically here
+  extern __shared__ int wc[];     // [16 waves][n_slots]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < 16 * n_slots; i += blockDim.x) wc[i] = 0;
+  __syncthreads();
+  int i = blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
+  int s = i < n ? checked_slot(slots, i, n_slots, nullptr) : -1;
+  int lower = 0, same = 0;
+  for (int l = 0; l < 64; ++l) {
+    int o = __shfl(s, l, 64);
+    lower += (l < lane && o == s) ? 1 : 0;
+    same += (o == s) ? 1 : 0;
+  }
+  if (s >= 0 && lower == 0) wc[wave * n_slots + s] = same;   // first lane of each slot records the count
+  __syncthreads();
+  if (s >= 0) {
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wc[w * n_slots + s];
+    int pos = base[(size_t)blockIdx.x * n_slots + s] + before + lower;
+    perm[pos] = i;
+    if (inv) inv[i] = pos;
+  }
+}
+
+int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
+                    int32_t* inv, int tile_rows, int32_t* tile_off, int32_t* status, hipStream_t st) {
+  int nchunks = (n + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK;
+  if (nchunks == 0) nchunks = 1;
+  dispatch_hist_kernel<<<nchunks, 1024, n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, status);
+  dispatch_scan_kernel<<<1, 1024, 2 * n_slots * sizeof(int), st>>>(hist, nchunks, n_slots, offsets, tile_rows,
+                                                                     tile_off);
+  if (n > 0)
+    dispatch_place_kernel<<<nchunks, 1024, 16 * n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, perm, inv);
+  return check_launch("prefill dispatch");
+}
+
+size_t dispatch_workspace(int n, int n_slots) {
+  int nchunks = (n + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK;
+  if (nchunks == 0) nchunks = 1;
+  return align256((size_t)nchunks * n_slots * sizeof(int32_t));
+}
+
+int launch_router_small(const RouterSmallArgs& a, hipStream_t st) {
+  int nquant = a.xq_hi ? (int)(((int64_t)a.T * (a.H / 32) + 255) / 256) : 0;
+  router_small_kernel<<<a.nlog + nquant, 256, 0, st>>>(a);
+  return check_launch("router_small");
+}
+
+int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st) {
+  dim3 grid((E + 63) / 64, (T + 31) / 32);
+  router_logits_kernel<<<grid, 256, 0, st>>>(x, W, T, H, E, logits);
+  return check_launch("router_logits");
+}
+
+int launch_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling, int32_t* inds,
+                         float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
+                         hipStream_t st) {
+  int blocks = (T + 3) / 4;
+  router_select_kernel<<<blocks, 256, 4 * 2 * E * sizeof(float), st>>>(logits, bias, T, E, k, scaling, inds, w,
+                                                                         slot_of, slot_inds, n_slots, status);
+  return check_launch("router_select");
+}
+
+}  // namespace mimo
+
+using namespace mimo;
+
+extern "C" {
+
+int mimo_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling, int32_t* inds,
+                       float* w, void* stream) {
+  MIMO_REQUIRE(logits && bias && inds && w, MIMO_ERR_ARG, "router_select: null pointer");
+  MIMO_REQUIRE(T >= 0 && E >= 1 && E <= 1024 && k >= 1 && k <= 16 && k <= E, MIMO_ERR_SHAPE,
+               "router_select: need 1 <= k <= min(16, E), E <= 1024");
+  if (T == 0) return MIMO_OK;
+  return launch_router_select(logits, bias, T, E, k, scaling, inds, w, nullptr, nullptr, 0, nullptr,
+                              as_stream(stream));
+}
+
+int mimo_router(const uint16_t* x, const uint16_t* Wg, const float* bias, int T, int H, int E, int k, float* logits,
+                int32_t* inds, float* w, void* stream) {
+  MIMO_REQUIRE(x && Wg && bias && logits && inds && w, MIMO_ERR_ARG, "router: null pointer");
+  MIMO_REQUIRE(T >= 0 && H >= 64 && H % 64 == 0 && E >= 1 && E <= 1024 && k >= 1 && k <= 16 && k <= E,
+               MIMO_ERR_SHAPE, "router: need H %% 64 == 0, 1 <= k <= min(16, E), E <= 1024");
+  if (T == 0) return MIMO_OK;
+  hipStream_t st = as_stream(stream);
+  int rc = launch_router_logits(x, Wg, T, H, E, logits, st);
+  if (rc) return rc;
+  return launch_router_select(logits, bias, T, E, k, 1.0f, inds, w, nullptr, nullptr, 0, nullptr, st);
+}
+
+int mimo_group_routes(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k, int R,
+                      int n_slots, int32_t* uids, int32_t* urows, int32_t* ucnt, float* uw, uint32_t* gidx,
+                      int32_t* n_unique, int32_t* status, void* stream) {
+  MIMO_REQUIRE(inds && scores && uids && urows && ucnt && uw && gidx && n_unique && status, MIMO_ERR_ARG,
+               "group_routes: null pointer");
+  MIMO_REQUIRE(M >= 1 && k >= 1 && M * k <= 1024 && R >= 1 && n_slots >= 1 && n_slots <= 1024, MIMO_ERR_SHAPE,
+               "group_routes: need 1 <= M*k <= 1024, 1 <= n_slots <= 1024");
+  int Umax = M * k < n_slots ? M * k : n_slots;
+  group_routes_kernel<<<1, 1024, 0, as_stream(stream)>>>(inds, scores, slot_of, M, k, R, n_slots, Umax, uids, urows,
+                                                         ucnt, uw, gidx, n_unique, status);
+  return check_launch("group_routes");
+}
+
+size_t mimo_prefill_dispatch_workspace_size(int T, int k, int n_slots) {
+  return dispatch_workspace(T * k, n_slots);
+}
+
+int mimo_prefill_dispatch(const int32_t* slot_inds, int T, int k, int n_slots, int32_t* perm, int32_t* offsets,
+                          int32_t* inv, void* ws, size_t ws_bytes, void* stream) {
+  MIMO_REQUIRE(slot_inds && perm && offsets, MIMO_ERR_ARG, "prefill_dispatch: null pointer");
+  MIMO_REQUIRE(T >= 0 && k >= 1 && n_slots >= 1 && n_slots <= 1024, MIMO_ERR_SHAPE,
+               "prefill_dispatch: need 1 <= n_slots <= 1024");
+  MIMO_REQUIRE(ws && ws_bytes >= dispatch_workspace(T * k, n_slots), MIMO_ERR_WORKSPACE,
+               "prefill_dispatch: workspace too small");
+  return launch_dispatch(slot_inds, T * k, n_slots, static_cast<int32_t*>(ws), perm, offsets, inv, 0, nullptr,
+                         nullptr, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+"""ctypes binding of libmimo_moe.so (the C ABI declared in include/mimo_moe.h).
+
+The library is the only compute path: if it is not built this module raises, there is no fallback.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmimo_moe.so")
+ABI_VERSION = 1
+
+MIMO_OK = 0
+ERR_SHAPE, ERR_ALIGN, ERR_ROWS_PER_EXPERT, ERR_SLOT, ERR_WORKSPACE, ERR_HIP, ERR_ARG = -1, -2, -3, -4, -5, -6, -7
+_VALUE_ERRORS = {ERR_SHAPE, ERR_ALIGN, ERR_ROWS_PER_EXPERT, ERR_SLOT, ERR_WORKSPACE, ERR_ARG}
+
+
+class MimoBank(ctypes.Structure):
+    """struct mimo_bank (include/mimo_moe.h)."""
+    _fields_ = [("gate_w", ctypes.c_void_p), ("gate_s", ctypes.c_void_p),
+                ("up_w", ctypes.c_void_p), ("up_s", ctypes.c_void_p),
+                ("down_w", ctypes.c_void_p), ("down_s", ctypes.c_void_p),
+                ("n_slots", ctypes.c_int32), ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32)]
+
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+U64 = ctypes.c_uint64
+F32 = ctypes.c_float
+SZ = ctypes.c_size_t
+BANKP = ctypes.POINTER(MimoBank)
+
+SIGNATURES = {
+    "mimo_abi_version": (I32, []),
+    "mimo_last_error": (ctypes.c_char_p, []),
+    "mimo_quantize_mxfp4": (I32, [P, I64, I64, P, P, P]),
+    "mimo_dequantize_mxfp4": (I32, [P, P, I64, I64, P, P]),
+    "mimo_random_bf16": (I32, [U64, F32, I64, P, P]),
+    "mimo_fill_random_mxfp4": (I32, [U64, F32, I64, I64, P, P, P]),
+    "mimo_quantize_fp8_hilo": (I32, [P, I64, I64, P, P, P, P, P]),
+    "mimo_sigmoid_table": (I32, [P, P]),
+    "mimo_router_select": (I32, [P, P, I32, I32, I32, F32, P, P, P]),
+    "mimo_router": (I32, [P, P, P, I32, I32, I32, I32, P, P, P, P]),
+    "mimo_group_routes": (I32, [P, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, P]),
+    "mimo_prefill_dispatch": (I32, [P, I32, I32, I32, P, P, P, P, SZ, P]),
+    "mimo_prefill_dispatch_workspace_size": (SZ, [I32, I32, I32]),
+    "mimo_moe_experts": (I32, [P, I32, BANKP, P, P, P, P, P, I32, I32, P, I32, I32, P, P, P, P, SZ, P]),
+    "mimo_moe_experts_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
+    "mimo_moe_decode": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, SZ, P]),
+    "mimo_moe_decode_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
+    "mimo_moe_prefill": (I32, [P, I32, P, P, I32, BANKP, P, P, SZ, P]),
+    "mimo_moe_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
+    "mimo_moe_prefill_block": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, SZ, P]),
+    "mimo_moe_prefill_block_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Load and bind libmimo_moe.so; raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                                   "(or python mimo-on-a-mac_amd/build.py)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            if lib.mimo_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"libmimo_moe ABI {lib.mimo_abi_version()} != {ABI_VERSION}")
+            _lib = lib
+    return _lib
+
+
+def check(rc, what=""):
+    if rc == MIMO_OK:
+        return
+    msg = load().mimo_last_error().decode(errors="replace")
+    if rc in _VALUE_ERRORS:
+        raise ValueError(f"{what}: {msg} (code {rc})")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def call(name, *args):
+    check(getattr(load(), name)(*args), name)
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_ptr(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("libmimo_moe works on device tensors; got a CPU tensor")
+
+
+_ws = {}
+
+
+def workspace(nbytes, device, tag):
+    """Zeroed device workspace of at least nbytes, cached per (device, stream, entry point tag).
+
+    The kernels leave their counters at zero, so a buffer is zeroed only when it is (re)allocated; each entry
+    point gets its own buffer because their layouts differ."""
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream, tag)
+    buf = _ws.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _ws[key] = buf
+    return buf

@@ -1,0 +1,172 @@
+"""The MoE block of MiMo-V2.6-Flash on MI355X: Router and the decode / prefill dispatch of one MoE layer.
+
+Mirrors engine/mimo_stream/model.py:
+  Router                 :52-65   fp32 gate linear, sigmoid, noaux bias for selection, top-8, renormalised weights
+  MoEBlock._moe_small    :184-219 T <= VERIFY_MAX rows: M == 1 gather_qmm rounding, M >= 2 distinct-expert kernels
+  MoEBlock._moe_prefill  :230-271 stable sort of (token, k) routes by slot, grouped GEMMs, fixed-order combine
+  MoEBlock.__call__      :303-340 router -> small or prefill path (the caller adds y to the residual, :340)
+with every expert resident in HBM, so SlotCache.resolve / SSD reads (:191-217) reduce to the slot table.
+Unlike the reference, routes never go back to the host: routing, grouping and dispatch run on the device
+between the router and the expert kernels (the reference syncs at :315).
+"""
+import numpy as np
+import torch
+
+from . import _lib
+from .pools import E, TOPK, VERIFY_MAX, bank_struct
+
+
+class Router:
+    """Router (model.py:52-65): weight bf16 [E, H], e_score_correction_bias fp32 [E]."""
+
+    def __init__(self, hidden, n_experts=E, top_k=TOPK, device="cuda"):
+        self.weight = torch.zeros((n_experts, hidden), dtype=torch.bfloat16, device=device)
+        self.e_score_correction_bias = torch.zeros(n_experts, dtype=torch.float32, device=device)
+        self.top_k = top_k
+
+    def logits_and_routes(self, r):
+        """r bf16 [..., T, H] -> (logits fp32 [T, E], inds int32 [T, k], w fp32 [T, k])."""
+        _lib.require_cuda(r)
+        r2 = r.reshape(-1, r.shape[-1]).to(torch.bfloat16).contiguous()
+        T, H = r2.shape
+        En = self.weight.shape[0]
+        dev = r2.device
+        logits = torch.empty((T, En), dtype=torch.float32, device=dev)
+        inds = torch.empty((T, self.top_k), dtype=torch.int32, device=dev)
+        w = torch.empty((T, self.top_k), dtype=torch.float32, device=dev)
+        _lib.call("mimo_router", _lib.ptr(r2), _lib.ptr(self.weight.contiguous()),
+                  _lib.ptr(self.e_score_correction_bias.contiguous()), T, H, En, self.top_k, _lib.ptr(logits),
+                  _lib.ptr(inds), _lib.ptr(w), _lib.stream_ptr(dev))
+        return logits, inds, w
+
+    def __call__(self, r):
+        _, inds, w = self.logits_and_routes(r)
+        lead = r.shape[:-1]
+        return inds.reshape(*lead, self.top_k), w.reshape(*lead, self.top_k)
+
+
+def select_from_logits(logits, bias, k, scaling=1.0):
+    """Selection given fp32 logits [T, E] (model.py:60-64): inds int32 [T, k], w fp32 [T, k]."""
+    _lib.require_cuda(logits)
+    logits = logits.to(torch.float32).contiguous()
+    T, En = logits.shape
+    bias = bias.to(device=logits.device, dtype=torch.float32).contiguous()
+    inds = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    _lib.call("mimo_router_select", _lib.ptr(logits), _lib.ptr(bias), T, En, k, float(scaling), _lib.ptr(inds),
+              _lib.ptr(w), _lib.stream_ptr(logits.device))
+    return inds, w
+
+
+def prefill_dispatch(slot_inds, n_slots):
+    """Stable sort of the flat (token, k) routes by slot (model.py:235-242) and its inverse (:266-268):
+    perm int32 [T*k], offsets int32 [n_slots + 1], inv int32 [T*k]."""
+    _lib.require_cuda(slot_inds)
+    si = slot_inds.to(torch.int32).contiguous()
+    T, k = si.shape
+    dev = si.device
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_slots + 1, dtype=torch.int32, device=dev)
+    nbytes = _lib.load().mimo_prefill_dispatch_workspace_size(T, k, n_slots)
+    ws = _lib.workspace(nbytes, dev, "dispatch")
+    _lib.call("mimo_prefill_dispatch", _lib.ptr(si), T, k, n_slots, _lib.ptr(perm), _lib.ptr(offsets), _lib.ptr(inv),
+              _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+    return perm, offsets, inv
+
+
+class MoEBlock:
+    """One MoE layer: router, resident slot bank and expert -> slot table (slot_of None = identity)."""
+
+    def __init__(self, router, bank, slot_of=None):
+        self.router = router
+        self.bank = bank
+        self.slot_of = None if slot_of is None else torch.as_tensor(slot_of, dtype=torch.int32).to(
+            router.weight.device).contiguous()
+        self._bank_struct = bank_struct(bank)
+
+    @property
+    def n_slots(self):
+        return self._bank_struct.n_slots
+
+    def _slots(self, inds):
+        inds = inds.to(torch.int64)
+        return (self.slot_of[inds] if self.slot_of is not None else inds).to(torch.int32).contiguous()
+
+    def _moe_small(self, r2, inds, w):
+        """T <= VERIFY_MAX rows with given routes (model.py:184-219): M == 1 rounds each expert's output to bf16
+        (_gather_m1), M >= 2 sums fp32 partials (distinct-expert kernels).  No host synchronisation."""
+        _lib.require_cuda(r2)
+        T, k = inds.shape
+        if T > VERIFY_MAX:
+            raise ValueError(f"_moe_small takes at most {VERIFY_MAX} rows")
+        dev = r2.device
+        S = self.n_slots
+        slot_inds = self._slots(inds)
+        w = w.to(torch.float32).contiguous()
+        Umax = min(T * k, S)
+        R = VERIFY_MAX
+        uids = torch.empty(Umax, dtype=torch.int32, device=dev)
+        urows = torch.empty((Umax, R), dtype=torch.int32, device=dev)
+        ucnt = torch.empty(Umax, dtype=torch.int32, device=dev)
+        uw = torch.empty((Umax, R), dtype=torch.float32, device=dev)
+        gidx = torch.empty(T * k, dtype=torch.int32, device=dev)
+        nu = torch.empty(2, dtype=torch.int32, device=dev)
+        st = _lib.stream_ptr(dev)
+        _lib.call("mimo_group_routes", _lib.ptr(slot_inds), _lib.ptr(w), None, T, k, R, S, _lib.ptr(uids),
+                  _lib.ptr(urows), _lib.ptr(ucnt), _lib.ptr(uw), _lib.ptr(gidx), _lib.ptr(nu[0:1]), _lib.ptr(nu[1:2]), st)
+        x = r2.to(torch.bfloat16).contiguous()
+        y = torch.empty((T, self._bank_struct.hidden), dtype=torch.bfloat16, device=dev)
+        H, I = self._bank_struct.hidden, self._bank_struct.inter
+        nbytes = _lib.load().mimo_moe_experts_workspace_size(T, Umax, R, H, I)
+        ws = _lib.workspace(nbytes, dev, "experts")
+        _lib.call("mimo_moe_experts", _lib.ptr(x), T, self._bank_struct, _lib.ptr(uids), _lib.ptr(urows), _lib.ptr(ucnt),
+                  _lib.ptr(uw), _lib.ptr(nu[0:1]), Umax, R, _lib.ptr(gidx), k, 1 if T == 1 else 0, _lib.ptr(y), None,
+                  None, _lib.ptr(ws), ws.numel(), st)
+        return y
+
+    def _moe_prefill(self, r2, inds, w):
+        """Prefill with given routes (model.py:230-271): [T, H] bf16."""
+        _lib.require_cuda(r2)
+        T, k = inds.shape
+        dev = r2.device
+        x = r2.to(torch.bfloat16).contiguous()
+        slot_inds = self._slots(inds)
+        w = w.to(torch.float32).contiguous()
+        b = self._bank_struct
+        y = torch.empty((T, b.hidden), dtype=torch.bfloat16, device=dev)
+        nbytes = _lib.load().mimo_moe_prefill_workspace_size(T, k, b.n_slots, b.hidden, b.inter)
+        ws = _lib.workspace(nbytes, dev, "prefill")
+        _lib.call("mimo_moe_prefill", _lib.ptr(x), T, _lib.ptr(slot_inds), _lib.ptr(w), k, b, _lib.ptr(y), _lib.ptr(ws),
+                  ws.numel(), _lib.stream_ptr(dev))
+        return y
+
+    def __call__(self, r, return_routes=False):
+        """Router + experts for r bf16 [T, H] (model.py:303-336): T <= 8 runs the fused decode block, larger T
+        the prefill block.  Returns y bf16 [T, H] (and inds, w when return_routes)."""
+        _lib.require_cuda(r)
+        r2 = r.reshape(-1, r.shape[-1]).to(torch.bfloat16).contiguous()
+        T = r2.shape[0]
+        dev = r2.device
+        b = self._bank_struct
+        rt = self.router
+        En, k = rt.weight.shape[0], rt.top_k
+        y = torch.empty((T, b.hidden), dtype=torch.bfloat16, device=dev)
+        inds = torch.empty((T, k), dtype=torch.int32, device=dev)
+        w = torch.empty((T, k), dtype=torch.float32, device=dev)
+        st = _lib.stream_ptr(dev)
+        args = (_lib.ptr(r2), T, _lib.ptr(rt.weight), _lib.ptr(rt.e_score_correction_bias), _lib.ptr(self.slot_of), En, k,
+                b, _lib.ptr(y), _lib.ptr(inds), _lib.ptr(w))
+        if T <= VERIFY_MAX:
+            nbytes = _lib.load().mimo_moe_decode_workspace_size(T, En, k, b.hidden, b.inter)
+            ws = _lib.workspace(nbytes, dev, "decode")
+            _lib.call("mimo_moe_decode", *args, _lib.ptr(ws), ws.numel(), st)
+        else:
+            nbytes = _lib.load().mimo_moe_prefill_block_workspace_size(T, En, k, b.n_slots, b.hidden, b.inter)
+            ws = _lib.workspace(nbytes, dev, "prefill_block")
+            _lib.call("mimo_moe_prefill_block", *args, _lib.ptr(ws), ws.numel(), st)
+        return (y, inds, w) if return_routes else y
+
+    def forward_residual(self, x, r):
+        """h = x + MoE(r) (model.py:340)."""
+        return x + self(r).reshape(x.shape)

@@ -41,11 +41,15 @@ def exp_spec(x):
 
 
 def sigmoid_f32(logits):
-    """Elementwise fp32 sigmoid, exactly specified (see module docstring).  model.py:60."""
+    """Elementwise fp32 sigmoid, exactly specified (see module docstring); a NaN input gives the canonical
+    quiet NaN 0x7FC00000.  model.py:60."""
     x = np.asarray(logits, dtype=np.float32).astype(np.float64)
+    nan = np.isnan(x)
+    x = np.where(nan, 0.0, x)
     x = np.where(x < -SIGMOID_CLAMP, -SIGMOID_CLAMP, np.where(x > SIGMOID_CLAMP, SIGMOID_CLAMP, x))
     e = exp_spec(-x)
-    return (1.0 / (1.0 + e)).astype(np.float32)
+    out = (1.0 / (1.0 + e)).astype(np.float32)
+    return np.where(nan, np.array([0x7FC00000], np.uint32).view(np.float32)[0], out).astype(np.float32)
 
 
 def router_logits(x_bf16_as_f32, W_bf16_as_f32):

@@ -25,6 +25,7 @@ def test_sigmoid_f32_matches_libm_rounding():
     np.testing.assert_array_equal(ours, ref)
     sp = routing.sigmoid_f32(np.array([np.inf, -np.inf, np.nan, 0.0], np.float32))
     assert sp[0] == 1.0 and sp[1] == 0.0 and np.isnan(sp[2]) and sp[3] == 0.5
+    assert sp[2:3].view(np.uint32)[0] == 0x7FC00000       # canonical quiet NaN
 
 
 def test_select_topk_set_matches_argpartition():
