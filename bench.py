@@ -1,0 +1,370 @@
+#!/usr/bin/env python3
+"""Benchmark of the MiMo-V2.6-Flash MoE block on one MI355X.
+
+Headline (`value`): MoE-layer decode throughput at 1 row on a MiMo-shaped layer (H=4096, E=256 experts all
+resident, I=2048, top-8, MXFP4 group 32), in algorithmic GB/s: per step the bytes of the distinct experts
+read (U x 13,369,344) plus the router weight (256 x 4096 x 2) plus the row in and out.  One step = one fused
+MoE-layer decode (router -> top-8 -> grouping -> experts -> combine) on a freshly routed row; steps rotate over
+`--layers` distinct resident layers so no step finds its experts in L2 / MALL.  The timed region is one replay
+of a HIP graph holding exactly --steps steps, inputs resident in HBM.
+
+Also reported (field "extra"): decode at 2, 4, 8 rows with controlled routing (consecutive rows share ~2.6
+of 8 experts), prefill at 512 / 2048 tokens with Zipf(1.1) expert popularity, a 48-layer stack decode at 1
+and 4 rows, and the per-kernel durations measured with HIP events.  "cpu_baseline" times the numpy oracle
+(the CPU restatement of the reference algorithm) on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps 500] [--warmup 20]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mimo-on-a-mac_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer decode GB/s (% HBM peak) at 1–8 rows; prefill tokens/sec"
+HBM_PEAK_GBS = 8000.0
+MXFP4_PEAK_TFLOPS = 10100.0
+FP8_PEAK_TFLOPS = 5000.0
+H, I, E, K = 4096, 2048, 256, 8
+ROUTER_BYTES = E * H * 2
+GATEUP_BYTES_PER_EXPERT = 2 * (I * H // 2 + I * H // 32)      # 8,912,896
+FLOPS_PER_ROUTE = 2 * (2 * I * H + H * I)                      # 50,331,648
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=48, help="resident MoE layers (48 = the MiMo stack)")
+    ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+class Layers:
+    """`n` resident MoE layers: 256-slot MXFP4 banks from seeded N(0, 0.02) weights, random bf16 routers."""
+
+    def __init__(self, n, device):
+        import torch
+        from mimo_stream import pools, kernels, Router, MoEBlock
+        self.blocks, self.W = [], []
+        for l in range(n):
+            bank = pools.random_bank(E, seed=1000 + l, device=device)
+            r = Router(H, E, K, device=device)
+            r.weight.copy_(kernels.random_bf16((E, H), seed=5000 + l, stddev=0.02, device=device))
+            self.blocks.append(MoEBlock(r, bank))
+            self.W.append(r.weight.float().cpu().numpy())
+        torch.cuda.synchronize()
+
+
+def steered_rows(rng, W, sets, alpha=6.0):
+    """Rows x ~ N(0, 1) plus alpha * sum of the unit router rows of `sets[i]` (float32; the caller rounds to
+    bf16): the router picks (almost always exactly) the experts in sets[i]; the realised routing is
+    measured and reported."""
+    import numpy as np
+    Wn = W / np.linalg.norm(W, axis=1, keepdims=True)
+    x = rng.standard_normal((len(sets), W.shape[1])).astype(np.float32)
+    for i, s in enumerate(sets):
+        x[i] += alpha * Wn[list(s)].sum(0)
+    return x
+
+
+def controlled_sets(rng, M, shared_cycle=(3, 2, 3, 3, 2)):
+    """Row 0: 8 random experts; row i keeps shared_cycle[i-1 mod 5] of row i-1's experts (mean 2.6) and draws
+    the rest fresh (the verify-width routing statistics of bench/results/raw/mimo-cache-sim.json:313-338)."""
+    import numpy as np
+    sets = [list(rng.choice(E, K, replace=False))]
+    for i in range(1, M):
+        keep = shared_cycle[(i - 1) % len(shared_cycle)]
+        kept = list(rng.choice(sets[-1], keep, replace=False))
+        pool = np.setdiff1d(np.arange(E), sets[-1])
+        sets.append(kept + list(rng.choice(pool, K - keep, replace=False)))
+    return sets
+
+
+def time_graph(fn, steps, warmup):
+    """W eager warm-up steps, capture `steps` steps in one HIP graph, one untimed replay, then one timed
+    replay bracketed by synchronisation.  Returns ms per step."""
+    import torch
+    for s in range(warmup):
+        fn(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for s in range(steps):
+            fn(s)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    del g
+    return ms / steps
+
+
+def kernel_times(fn, steps):
+    """Per-kernel average durations (ms) over `steps` eager steps, from HIP events the library records on
+    its launch stream."""
+    import torch
+    from mimo_stream import _lib
+    torch.cuda.synchronize()
+    _lib.profile_enable(True)
+    for s in range(steps):
+        fn(s)
+    prof = _lib.profile_read()
+    _lib.profile_enable(False)
+    return {k: (t / n, n) for k, (t, n) in prof.items()}
+
+
+def decode_case(layers, M, steps, warmup, seed, device):
+    """Fused decode of M rows per step, layers rotated.  Returns dict with ms/step, realised U, GB/s."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(seed)
+    n = len(layers.blocks)
+    nin = steps
+    X = np.zeros((nin, M, H), np.float32)
+    for s in range(nin):
+        l = s % n
+        sets = controlled_sets(rng, M)
+        X[s] = steered_rows(rng, layers.W[l], sets)
+    Xd = torch.from_numpy(X).to(torch.bfloat16).to(device)
+    blocks = layers.blocks
+
+    def fn(s):
+        blocks[s % n](Xd[s % nin])
+
+    # realised routing on a sample of steps
+    Us, shared = [], []
+    for s in range(min(nin, 64)):
+        _, inds, _ = blocks[s % n](Xd[s], return_routes=True)
+        ii = inds.cpu().numpy()
+        Us.append(len(np.unique(ii)))
+        for r in range(1, M):
+            shared.append(len(set(ii[r]) & set(ii[r - 1])))
+    U = float(np.mean(Us))
+    ms = time_graph(fn, steps, warmup)
+    nbytes = U * 13369344 + ROUTER_BYTES + 2 * M * H * 2
+    return {"rows": M, "ms_per_layer": ms, "distinct_experts": U,
+            "shared_with_previous_row": float(np.mean(shared)) if shared else None,
+            "naive_per_row_experts": M * K,
+            "GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "experts_only_GBps": U * 13369344 / (ms * 1e-3) / 1e9, "_fn": fn, "_U": U}
+
+
+def prefill_case(layers, T, steps, warmup, seed, device):
+    """Expert path of prefill (dispatch + grouped GEMMs + combine) with Zipf(1.1) routes, layers rotated."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(seed)
+    n = min(len(layers.blocks), 8)
+    nin = 4
+    perm = rng.permutation(E)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    logp = np.log(p / p.sum())
+    Xs, Is, Ws, Us = [], [], [], []
+    for _ in range(nin):
+        g = rng.gumbel(size=(T, E)) + logp[None, :]
+        inds = perm[np.argsort(-g, axis=1)[:, :K]].astype(np.int32)
+        w = rng.random((T, K)).astype(np.float32)
+        w /= w.sum(1, keepdims=True)
+        Xs.append(torch.randn(T, H, device=device).to(torch.bfloat16))
+        Is.append(torch.from_numpy(inds).to(device))
+        Ws.append(torch.from_numpy(w).to(device))
+        Us.append(len(np.unique(inds)))
+    blocks = layers.blocks
+
+    def fn(s):
+        blocks[s % n]._moe_prefill(Xs[s % nin], Is[s % nin], Ws[s % nin])
+
+    ms = time_graph(fn, steps, warmup)
+    U = float(np.mean(Us))
+    nbytes = U * 13369344 + 2 * T * H * 2
+    flops = T * K * FLOPS_PER_ROUTE
+    return {"tokens": T, "ms_per_layer": ms, "tokens_per_s": T / (ms * 1e-3), "distinct_experts": U,
+            "GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "TFLOPs": flops / (ms * 1e-3) / 1e12,
+            "mxfp4_mfma_frac": flops / (ms * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS, "_fn": fn}
+
+
+def stack_case(layers, M, tokens, device, seed):
+    """One decode step through every resident layer (48 = the MiMo stack): per-layer steered hidden states
+    with Zipf(1.1) expert popularity; reports MoE time per token and aggregate GB/s."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(seed)
+    n = len(layers.blocks)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    Xd, Us = [], []
+    for t in range(tokens):
+        for l in range(n):
+            perm = np.random.default_rng(10 * l + 1).permutation(E)
+            sets = [list(perm[rng.choice(E, K, replace=False, p=p)]) for _ in range(M)]
+            Xd.append(torch.from_numpy(steered_rows(rng, layers.W[l], sets)).to(torch.bfloat16).to(device))
+            Us.append(len(np.unique(np.concatenate(sets))))
+    blocks = layers.blocks
+
+    def fn(s):
+        blocks[s % n](Xd[s % len(Xd)])
+
+    steps = n * tokens
+    ms = time_graph(fn, steps, warmup=n)
+    U = float(np.mean(Us))
+    nbytes = U * 13369344 + ROUTER_BYTES + 2 * M * H * 2
+    return {"layers": n, "rows": M, "ms_per_token": ms * n, "distinct_experts_per_layer": U,
+            "GBps": nbytes * n / (ms * n * 1e-3) / 1e9,
+            "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch measured with rocprofv3 counters (committed summary), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return d.get(f"{kernel}:{workload}")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(layers, seconds):
+    """The numpy oracle (CPU restatement of Router + _gather_m1, model.py:58-65, :173-182) on M = 1 decode
+    steps of the same layers, one thread, for about `seconds`; returns GB/s with the same byte accounting."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from oracle import experts as ox, routing as orr, mxfp4 as oq
+    rng = np.random.default_rng(7)
+    done, t_cpu, nbytes = 0, 0.0, 0.0
+    blocks = layers.blocks
+    with threadpool_limits(1):
+        while t_cpu < seconds and done < 50:
+            l = done % len(blocks)
+            x = oq.round_bf16(steered_rows(rng, layers.W[l], controlled_sets(rng, 1)))
+            _, inds, _ = blocks[l](torch.from_numpy(x).to(torch.bfloat16).cuda(), return_routes=True)
+            sel = inds.cpu().numpy()[0]
+            b = blocks[l].bank
+            idx = torch.from_numpy(sel.astype(np.int64)).cuda()
+            sub = {k: v[idx].cpu().numpy() for k, v in b.items()}          # staging, not timed
+            sub = {k: (v.view(np.uint32) if k.endswith("_w") else v) for k, v in sub.items()}
+            t0 = time.perf_counter()
+            logits = orr.router_logits(x, layers.W[l])
+            oi, ow = orr.select_topk(logits, np.zeros(E, np.float32), K)
+            pool = ox.ExpertPool(sub)
+            remap = {int(e): j for j, e in enumerate(sel)}
+            slots = np.array([remap.get(int(e), 0) for e in oi[0]])
+            ox.gather_m1(x[0], pool, slots, ow[0])
+            t_cpu += time.perf_counter() - t0
+            done += 1
+            nbytes += len(np.unique(oi[0])) * 13369344 + ROUTER_BYTES + 2 * H * 2
+    return {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} one-row MoE-layer decode steps (router + 8 MXFP4 experts + combine) of the same "
+                      f"layers, numpy oracle, 1 thread, {t_cpu:.1f} s of CPU time; host has {os.cpu_count()} "
+                      f"logical CPUs ({_cpu_model()})"}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the MoE block runs on a single MI355X "
+                                   "(multi-GPU sharding is described in DESIGN.md, not implemented)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device"}))
+        sys.exit(1)
+    device = "cuda:0"
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    layers = Layers(args.layers, device)
+    log(f"[bench] {args.layers} layers resident ({args.layers * E * 13369344 / 1e9:.1f} GB) in {time.time() - t0:.1f}s")
+
+    head = decode_case(layers, 1, args.steps, args.warmup, seed=1, device=device)
+    log(f"[bench] decode M=1: {head['ms_per_layer'] * 1e3:.1f} us/layer, {head['GBps']:.0f} GB/s")
+    kt = kernel_times(head["_fn"], min(args.steps, 200))
+    gu_ms, gu_n = kt.get("decode_gateup", (float("nan"), 0))
+    achieved = head["_U"] * GATEUP_BYTES_PER_EXPERT / (gu_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "kernel": "decode_gateup_kernel", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                "traffic": traffic_from_profiles("decode_gateup_kernel", "decode_m1"),
+                "bytes_per_launch": head["_U"] * GATEUP_BYTES_PER_EXPERT, "avg_us": gu_ms * 1e3,
+                "launches_timed": gu_n}
+
+    extra = {"kernel_us_decode_m1": {k: round(v[0] * 1e3, 2) for k, v in kt.items()}}
+    if not args.no_extra:
+        for M in (2, 4, 8):
+            try:
+                r = decode_case(layers, M, min(args.steps, 300), args.warmup, seed=10 + M, device=device)
+                r.pop("_fn"), r.pop("_U")
+                extra[f"decode_m{M}"] = r
+                log(f"[bench] decode M={M}: {r['ms_per_layer'] * 1e3:.1f} us/layer, U={r['distinct_experts']:.1f}, {r['GBps']:.0f} GB/s")
+            except Exception as e:    # an extra measurement never hides the headline
+                extra[f"decode_m{M}"] = {"error": repr(e)}
+        for T in (512, 2048):
+            try:
+                r = prefill_case(layers, T, 20, 3, seed=20 + T, device=device)
+                kt2 = kernel_times(r.pop("_fn"), 4)
+                r["kernel_us"] = {k: round(v[0] * 1e3, 1) for k, v in kt2.items()}
+                extra[f"prefill_t{T}"] = r
+                log(f"[bench] prefill T={T}: {r['ms_per_layer']:.3f} ms/layer, {r['tokens_per_s']:.0f} tok/s")
+            except Exception as e:
+                extra[f"prefill_t{T}"] = {"error": repr(e)}
+        for M in (1, 4):
+            try:
+                r = stack_case(layers, M, tokens=4, device=device, seed=30 + M)
+                extra[f"stack{args.layers}_m{M}"] = r
+                log(f"[bench] stack M={M}: {r['ms_per_token']:.3f} ms/token, {r['GBps']:.0f} GB/s")
+            except Exception as e:
+                extra[f"stack{args.layers}_m{M}"] = {"error": repr(e)}
+    head.pop("_fn"), head.pop("_U")
+    extra["decode_m1"] = head
+
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(layers, args.cpu_seconds)
+        except Exception as e:
+            cpu = {"error": repr(e)}
+
+    out = {
+        "metric": METRIC, "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_layer"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "mxfp4 x bf16 -> fp32 (block-scaled fp8/fp4 MFMA)", "data": "synthetic",
+        "config": {"workload": "MiMo-V2.6-Flash MoE layer decode, 1 row: router 4096->256 bf16, top-8, 256 "
+                               "resident MXFP4 experts (I=2048, group 32), SwiGLU, fixed-order combine",
+                   "hidden": H, "experts": E, "top_k": K, "intermediate": I, "rows": 1,
+                   "resident_layers": args.layers, "hbm_frac": head["hbm_frac"]},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -149,6 +149,16 @@ int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const f
                            int32_t* inds_out, float* w_out, void* ws, size_t ws_bytes, void* stream);
 size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, int H, int I);
 
+/* ---------------------------------------------------------------- measurement */
+
+/* No counterpart in the reference: per-kernel timing for benchmarks.  While enabled, every kernel launch is
+ * bracketed by HIP events on its stream (adds one event record per launch).  mimo_profile_enable also clears
+ * the records.  mimo_profile_read synchronises on the recorded events and returns the number of distinct
+ * kernel names; for the first max_kernels of them it writes the name (64 bytes each, NUL-terminated, host
+ * buffer), the total milliseconds and the launch count (host arrays). */
+int mimo_profile_enable(int on);
+int mimo_profile_read(int max_kernels, char* names, float* total_ms, int* launches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,8 @@
 // MXFP4 codec, seeded random pools, activation hi/lo split, bf16 sigmoid table, error state.
 #include <mutex>
 #include <string>
+#include <string.h>
+#include <vector>
 
 #include "device.h"
 #include "host.h"
@@ -20,6 +22,50 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 void clear_error() { g_err.clear(); }
+
+// ------------------------------------------------------------------ opt-in kernel timing
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+static std::mutex g_prof_mu;
+static bool g_prof_on = false;
+static std::vector<ProfRec> g_prof;
+static std::vector<hipEvent_t> g_prof_pool;
+static const char* g_prof_open = nullptr;
+static hipEvent_t g_prof_open_ev;
+
+static hipEvent_t prof_event() {
+  if (!g_prof_pool.empty()) {
+    hipEvent_t e = g_prof_pool.back();
+    g_prof_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+void prof_begin(hipStream_t st, const char* name) {
+  if (!g_prof_on) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  hipEvent_t e = prof_event();
+  if (!e) return;
+  hipEventRecord(e, st);
+  g_prof_open = name;
+  g_prof_open_ev = e;
+}
+
+void prof_end(hipStream_t st) {
+  if (!g_prof_on) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (!g_prof_open) return;
+  hipEvent_t e = prof_event();
+  if (!e) return;
+  hipEventRecord(e, st);
+  g_prof.push_back({g_prof_open, g_prof_open_ev, e});
+  g_prof_open = nullptr;
+}
 
 // ------------------------------------------------------------------ seeded normal generator
 // Element i of stream `seed`: splitmix64 of (seed, i) gives two 24-bit uniforms, Box-Muller gives N(0,1).
@@ -165,6 +211,7 @@ int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint
                              uint8_t* ls, hipStream_t st) {
   int64_t nb = rows * (cols / 32);
   if (nb == 0) return MIMO_OK;
+  ProfScope p(st, "quantize_fp8_hilo");
   quantize_fp8_hilo_kernel<<<(int)((nb + 255) / 256), 256, 0, st>>>(x, nb, hi, hs, lo, ls);
   return check_launch("quantize_fp8_hilo");
 }
@@ -213,6 +260,42 @@ using namespace mimo;
 extern "C" {
 
 int mimo_abi_version(void) { return MIMO_ABI_VERSION; }
+
+int mimo_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  for (auto& r : g_prof) { g_prof_pool.push_back(r.a); g_prof_pool.push_back(r.b); }
+  g_prof.clear();
+  g_prof_open = nullptr;
+  g_prof_on = on != 0;
+  return MIMO_OK;
+}
+
+int mimo_profile_read(int max_kernels, char* names, float* total_ms, int* launches) {
+  MIMO_REQUIRE(max_kernels >= 0 && (max_kernels == 0 || (names && total_ms && launches)), MIMO_ERR_ARG,
+               "profile_read: null pointer");
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  std::vector<const char*> keys;
+  std::vector<double> tot;
+  std::vector<int> cnt;
+  for (auto& r : g_prof) {
+    if (hipEventSynchronize(r.b) != hipSuccess) return set_error(MIMO_ERR_HIP, "profile_read: event sync failed");
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return set_error(MIMO_ERR_HIP, "profile_read: elapsed");
+    size_t j = 0;
+    while (j < keys.size() && strcmp(keys[j], r.name) != 0) ++j;
+    if (j == keys.size()) { keys.push_back(r.name); tot.push_back(0.0); cnt.push_back(0); }
+    tot[j] += ms;
+    cnt[j] += 1;
+  }
+  int n = (int)keys.size() < max_kernels ? (int)keys.size() : max_kernels;
+  for (int j = 0; j < n; ++j) {
+    strncpy(names + 64 * j, keys[j], 63);
+    names[64 * j + 63] = 0;
+    total_ms[j] = (float)tot[j];
+    launches[j] = cnt[j];
+  }
+  return (int)keys.size();
+}
 const char* mimo_last_error(void) { return g_err.c_str(); }
 
 static int grid_for(int64_t n, int threads) { return (int)((n + threads - 1) / threads); }

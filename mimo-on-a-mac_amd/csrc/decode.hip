@@ -262,9 +262,10 @@ static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream
   ExpertsArgs a = base;
   a.round_bf16 = round_bf16;
   dim3 g1(a.I / 32, a.Umax), g2(a.H / 64, a.Umax), g3((a.H + 1023) / 1024, M);
-  decode_gateup_kernel<<<g1, 256, 0, st>>>(a);
-  decode_down_kernel<<<g2, 256, 0, st>>>(a);
-  decode_combine_kernel<<<g3, 256, 0, st>>>(a.part, a.gidx, a.k, a.H, (uint32_t)(a.Umax * a.R), a.y);
+  { ProfScope p(st, "decode_gateup"); decode_gateup_kernel<<<g1, 256, 0, st>>>(a); }
+  { ProfScope p(st, "decode_down"); decode_down_kernel<<<g2, 256, 0, st>>>(a); }
+  { ProfScope p(st, "decode_combine");
+    decode_combine_kernel<<<g3, 256, 0, st>>>(a.part, a.gidx, a.k, a.H, (uint32_t)(a.Umax * a.R), a.y); }
   return check_launch("moe experts");
 }
 

@@ -23,6 +23,16 @@ inline int check_launch(const char* what) {
   return MIMO_OK;
 }
 
+// Opt-in per-kernel timing: when enabled (mimo_profile_enable), every launch site brackets its kernel with
+// HIP events on the launch stream; mimo_profile_read aggregates durations per kernel name.
+void prof_begin(hipStream_t st, const char* name);
+void prof_end(hipStream_t st);
+struct ProfScope {
+  hipStream_t st;
+  ProfScope(hipStream_t s, const char* name) : st(s) { prof_begin(s, name); }
+  ~ProfScope() { prof_end(st); }
+};
+
 // Device address of the bf16 sigmoid table (built on first use on the current device).
 const uint16_t* sigtab_device(int* err);
 

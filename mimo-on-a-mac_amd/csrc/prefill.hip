@@ -313,9 +313,10 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   a.hq_hi = ws.hq_hi; a.hq_lo = ws.hq_lo; a.hq_hs = ws.hq_hs; a.hq_ls = ws.hq_ls;
   a.Y = ws.Y; a.y = y;
   const int max_tiles = (P + PF_ROWS - 1) / PF_ROWS + S;     // bound on sum_s ceil(count_s / PF_ROWS)
-  prefill_gateup_kernel<<<dim3(I / 128, max_tiles), 256, 0, st>>>(a);
-  prefill_down_kernel<<<dim3(H / 128, max_tiles), 256, 0, st>>>(a);
-  prefill_combine_kernel<<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, y);
+  { ProfScope p(st, "prefill_gateup"); prefill_gateup_kernel<<<dim3(I / 128, max_tiles), 256, 0, st>>>(a); }
+  { ProfScope p(st, "prefill_down"); prefill_down_kernel<<<dim3(H / 128, max_tiles), 256, 0, st>>>(a); }
+  { ProfScope p(st, "prefill_combine");
+    prefill_combine_kernel<<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, y); }
   return check_launch("moe prefill");
 }
 

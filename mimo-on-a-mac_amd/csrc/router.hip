@@ -402,6 +402,7 @@ int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int
                     int32_t* inv, int tile_rows, int32_t* tile_off, int32_t* status, hipStream_t st) {
   int nchunks = (n + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK;
   if (nchunks == 0) nchunks = 1;
+  ProfScope p(st, "prefill_dispatch");
   dispatch_hist_kernel<<<nchunks, 1024, n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, status);
   dispatch_scan_kernel<<<1, 1024, 2 * n_slots * sizeof(int), st>>>(hist, nchunks, n_slots, offsets, tile_rows,
                                                                      tile_off);
@@ -418,12 +419,14 @@ size_t dispatch_workspace(int n, int n_slots) {
 
 int launch_router_small(const RouterSmallArgs& a, hipStream_t st) {
   int nquant = a.xq_hi ? (int)(((int64_t)a.T * (a.H / 32) + 255) / 256) : 0;
+  ProfScope p(st, "router_small");
   router_small_kernel<<<a.nlog + nquant, 256, 0, st>>>(a);
   return check_launch("router_small");
 }
 
 int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st) {
   dim3 grid((E + 63) / 64, (T + 31) / 32);
+  ProfScope p(st, "router_logits");
   router_logits_kernel<<<grid, 256, 0, st>>>(x, W, T, H, E, logits);
   return check_launch("router_logits");
 }
@@ -432,6 +435,7 @@ int launch_router_select(const float* logits, const float* bias, int T, int E, i
                          float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
                          hipStream_t st) {
   int blocks = (T + 3) / 4;
+  ProfScope p(st, "router_select");
   router_select_kernel<<<blocks, 256, 4 * 2 * E * sizeof(float), st>>>(logits, bias, T, E, k, scaling, inds, w,
                                                                          slot_of, slot_inds, n_slots, status);
   return check_launch("router_select");

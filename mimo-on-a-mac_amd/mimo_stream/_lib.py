@@ -54,6 +54,8 @@ SIGNATURES = {
     "mimo_moe_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "mimo_moe_prefill_block": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, SZ, P]),
     "mimo_moe_prefill_block_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "mimo_profile_enable": (I32, [I32]),
+    "mimo_profile_read": (I32, [I32, P, P, P]),
 }
 
 _lib = None
@@ -124,3 +126,22 @@ def workspace(nbytes, device, tag):
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _ws[key] = buf
     return buf
+
+
+def profile_enable(on=True):
+    """Start (or stop) per-kernel event timing inside the library; starting clears earlier records."""
+    load().mimo_profile_enable(1 if on else 0)
+
+
+def profile_read(max_kernels=32):
+    """{kernel name: (total ms, launches)} of the launches recorded since profile_enable (synchronises)."""
+    names = ctypes.create_string_buffer(64 * max_kernels)
+    tot = (ctypes.c_float * max_kernels)()
+    cnt = (ctypes.c_int * max_kernels)()
+    n = load().mimo_profile_read(max_kernels, names, tot, cnt)
+    check(n if n < 0 else 0, "profile_read")
+    out = {}
+    for j in range(min(n, max_kernels)):
+        nm = names.raw[64 * j:64 * j + 64].split(b"\0")[0].decode()
+        out[nm] = (float(tot[j]), int(cnt[j]))
+    return out
