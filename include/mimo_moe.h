@@ -13,8 +13,8 @@
  * slot; slot_of maps expert id -> slot (engine/mimo_stream/cache.py:16-17).
  *
  * Workspaces: entry points that take (ws, ws_bytes) need a caller-owned device buffer of at least the size
- * the matching *_workspace_size() returns, ZEROED ONCE when allocated (the kernels leave their counters at
- * zero when they finish).  Calls that share one workspace must be ordered on one stream.
+ * the matching *_workspace_size() returns; its contents need no initialisation (every kernel writes what it
+ * later reads).  Calls that share one workspace must be ordered on one stream.
  */
 #ifndef MIMO_MOE_H
 #define MIMO_MOE_H

@@ -49,43 +49,74 @@ __device__ __forceinline__ v8i b_operand(uint4 b) { return v8i{(int)b.x, (int)b.
 #define MFMA_F8xF4(A, B, C, SA, SB) __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 0, 4, 0, (SA), 0, (SB))
 
 // ------------------------------------------------------------------ Kernel A: gate/up + SwiGLU
-// Block: one distinct expert u (blockIdx.y) x 32 outputs n (blockIdx.x).  Waves: 2 n-tiles x 2 K-halves.
-// Writes h (bf16, rounding points of kernels.py:79-82) and its hi/lo E4M3 split for the down projection.
-__global__ void __launch_bounds__(256) decode_gateup_kernel(ExpertsArgs a) {
+// Block (512 threads): one distinct expert u (blockIdx.y) x 32 outputs n (blockIdx.x).  Wave w: 16-output
+// tile (w & 1) x K-range (w >> 1) of 4.  A wave's K-range is NS MFMA steps of K = 128; all of its loads (16 B
+// of gate and of up weights per lane and step, the activation halves and the scale words) are issued in one
+// straight-line batch before the first MFMA, so a block keeps 8 x 16 KB of expert weights in flight.  Loads
+// never depend on the lane: padding rows read row 0 and are zeroed by selects.  K-range partials are summed
+// in a fixed order through LDS; the epilogue applies the bf16 rounding points of kernels.py:79-82 and writes
+// h and its hi/lo split.
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int g) { return (w >> (8 * g)) & 0xFFu; }
+// K split of the gate/up reduction: 4 ranges when H % 512 == 0, else 2; MFMA steps (K = 128) per range.
+__host__ __device__ inline int gateup_ksplit(int H) { return H % 512 == 0 ? 4 : 2; }
+__host__ __device__ inline int gateup_steps(int H) { return H / gateup_ksplit(H) / 128; }
+__device__ __forceinline__ uint4 zero_if(uint4 v, bool keep) {
+  return keep ? v : make_uint4(0, 0, 0, 0);
+}
+
+template <int NS>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a) {
   const int u = blockIdx.y;
-  const int U = a.n_unique ? *a.n_unique : a.Umax;
-  if (u >= U) return;
-  const int cnt = min(a.ucnt[u], a.R);
-  const int slot = a.uslot[u];
-  if (cnt <= 0 || slot < 0 || slot >= a.S) return;     // caller-supplied ids are range-checked
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
-  const int ntile = wave & 1, khalf = wave >> 1;
+  const int arow = min(i & 7, a.R - 1);
+  // the routing metadata is loaded in one round trip (u < Umax, so every address is valid)
+  const int U = a.n_unique ? *a.n_unique : a.Umax;
+  const int cnt_raw = a.ucnt[u];
+  const int slot = a.uslot[u];
+  int token = a.urows[u * a.R + arow];
+  if (u >= U) return;
+  const int cnt = min(cnt_raw, a.R);
+  if (cnt <= 0 || slot < 0 || slot >= a.S) return;     // caller-supplied ids are range-checked
+  const int ntile = wave & 1, kr = wave >> 1;
   const int nb = blockIdx.x * 32;
   const int n0 = nb + ntile * 16;
-  const int arow = i & 7;
-  const bool avalid = arow < cnt;
-  int token = avalid ? a.urows[u * a.R + arow] : 0;
-  token = (token < 0 || token >= a.M) ? 0 : token;
+  const bool avalid = (i & 7) < cnt;
+  token = (!avalid || token < 0 || token >= a.M) ? 0 : token;
   const uint8_t* abase = (i < 8 ? a.xq_hi : a.xq_lo) + (size_t)token * a.H;
   const uint8_t* ascl = (i < 8 ? a.xq_hs : a.xq_ls) + (size_t)token * (a.H / 32);
   const size_t brow = (size_t)slot * a.I + n0 + i;
-  const uint32_t* gw = a.gate_w + brow * (a.H / 8);
-  const uint32_t* upw = a.up_w + brow * (a.H / 8);
-  const uint8_t* gs = a.gate_s + brow * (a.H / 32);
-  const uint8_t* us = a.up_s + brow * (a.H / 32);
-  const int kspan = a.H / 2;
-  const int kbeg = khalf * kspan;
+  const bool kactive = kr < gateup_ksplit(a.H);     // wave-uniform
+  const int k0 = (kactive ? kr : 0) * NS * 128;
+  const int b0 = k0 / 32;
+  const uint4* gw = reinterpret_cast<const uint4*>(a.gate_w + brow * (a.H / 8)) + b0 + g;   // one uint4 per 32-block
+  const uint4* upw = reinterpret_cast<const uint4*>(a.up_w + brow * (a.H / 8)) + b0 + g;
+  const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.gate_s + brow * (a.H / 32) + b0);
+  const uint32_t* us = reinterpret_cast<const uint32_t*>(a.up_s + brow * (a.H / 32) + b0);
+  const uint4* xr = reinterpret_cast<const uint4*>(abase + k0) + g;        // 16-byte units
+  const uint32_t* xs = reinterpret_cast<const uint32_t*>(ascl + b0);
   v4f accg = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int k0 = kbeg; k0 < kbeg + kspan; k0 += 128) {
-    const int blk = k0 / 32 + g;
-    uint4 bg = *reinterpret_cast<const uint4*>(gw + k0 / 8 + 4 * g);
-    uint4 bu = *reinterpret_cast<const uint4*>(upw + k0 / 8 + 4 * g);
-    int sg = gs[blk], su = us[blk];
-    v8i A = a_operand(abase, k0, g, avalid);
-    int sa = avalid ? (int)ascl[blk] : 127;
-    accg = MFMA_F8xF4(A, b_operand(bg), accg, sa, sg);
-    accu = MFMA_F8xF4(A, b_operand(bu), accu, sa, su);
+  if (kactive) {
+    // weights (the HBM stream) for every step stay in registers; activations (L2-resident) are loaded
+    // PF steps ahead of their MFMA
+    constexpr int PF = NS < 4 ? NS : 4;
+    uint4 bg[NS], bu[NS], xa[PF], xb[PF];
+    uint32_t sgw[NS], suw[NS], saw[PF];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) { bg[s] = gw[4 * s]; bu[s] = upw[4 * s]; }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) { sgw[s] = gs[s]; suw[s] = us[s]; }
+#pragma unroll
+    for (int s = 0; s < PF; ++s) { xa[s] = xr[8 * s]; xb[s] = xr[8 * s + 4]; saw[s] = xs[s]; }
+    __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first MFMA
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint4 p = zero_if(xa[s % PF], avalid), q = zero_if(xb[s % PF], avalid);
+      const int sa = avalid ? (int)byte_of(saw[s % PF], g) : 127;
+      if (s + PF < NS) { xa[s % PF] = xr[8 * (s + PF)]; xb[s % PF] = xr[8 * (s + PF) + 4]; saw[s % PF] = xs[s + PF]; }
+      v8i A = {(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, (int)q.z, (int)q.w};
+      accg = MFMA_F8xF4(A, b_operand(bg[s]), accg, sa, (int)byte_of(sgw[s], g));
+      accu = MFMA_F8xF4(A, b_operand(bu[s]), accu, sa, (int)byte_of(suw[s], g));
+    }
   }
   float vg[4], vu[4];
 #pragma unroll
@@ -93,20 +124,21 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(ExpertsArgs a) {
     vg[q] = accg[q] + __shfl_xor(accg[q], 32, 64);
     vu[q] = accu[q] + __shfl_xor(accu[q], 32, 64);
   }
-  __shared__ float red[2][2][32][4];
+  __shared__ float red[3][2][2][32][4];   // [K-range 1..3][ntile][gate/up][lane][q]
   __shared__ float hl[8][32];
-  if (khalf == 1 && lane < 32) {
+  if (kr > 0 && lane < 32) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) { red[ntile][0][lane][q] = vg[q]; red[ntile][1][lane][q] = vu[q]; }
+    for (int q = 0; q < 4; ++q) { red[kr - 1][ntile][0][lane][q] = vg[q]; red[kr - 1][ntile][1][lane][q] = vu[q]; }
   }
   __syncthreads();
-  if (khalf == 0 && lane < 32) {
+  if (kr == 0 && lane < 32) {
     const int n = n0 + i;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = 4 * g + q;
-      float gsum = vg[q] + red[ntile][0][lane][q];
-      float usum = vu[q] + red[ntile][1][lane][q];
+      float gsum = vg[q], usum = vu[q];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) { gsum += red[j][ntile][0][lane][q]; usum += red[j][ntile][1][lane][q]; }
       uint16_t gt = f32_to_bf16(gsum);
       float gtf = bf16_to_f32(gt);
       float ut = round_bf16(usum);
@@ -154,75 +186,92 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(ExpertsArgs a) {
   }
 }
 
-// ------------------------------------------------------------------ Kernel B: down * router weight
-// Block: one distinct expert u (blockIdx.y) x 64 outputs m (blockIdx.x); one wave per 16 outputs, full K.
-__global__ void __launch_bounds__(256) decode_down_kernel(ExpertsArgs a) {
-  const int u = blockIdx.y;
-  const int U = a.n_unique ? *a.n_unique : a.Umax;
-  if (u >= U) return;
-  const int cnt = min(a.ucnt[u], a.R);
-  const int slot = a.uslot[u];
-  if (cnt <= 0 || slot < 0 || slot >= a.S) return;
+// ------------------------------------------------------------------ Kernel B + combine (owner computes)
+// Block (1024 threads, 16 waves) owns 16 outputs m (blockIdx.x) for every distinct expert.  Work item
+// (u, K-half): wave w takes items w, w + 16, ...; per item its NS = I / 256 weight steps are loaded in one
+// batch, the activations a few steps ahead of their MFMA.  The two K-half dot products of each (expert,
+// row) land in LDS; the block adds them in a fixed order, applies the router weight (and the bf16 rounding
+// of the gather_qmm path when asked, model.py:181), sums each row's k routes in route order
+// (kernels.py:198-199) and writes y.  No other block is waited for.
+template <int NS>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) decode_down_combine_kernel(ExpertsArgs a) {
+  extern __shared__ float plds[];     // [2][Umax * R][16] K-half dot products
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
-  const int m0 = blockIdx.x * 64 + wave * 16;
+  const int m0 = blockIdx.x * 16;
   const int arow = i & 7;
-  const bool avalid = arow < cnt;
-  const size_t hrow = (size_t)u * a.R + arow;
-  const uint8_t* abase = (i < 8 ? a.hq_hi : a.hq_lo) + hrow * a.I;
-  const uint8_t* ascl = (i < 8 ? a.hq_hs : a.hq_ls) + hrow * (a.I / 32);
-  const size_t brow = (size_t)slot * a.H + m0 + i;
-  const uint32_t* dw = a.down_w + brow * (a.I / 8);
-  const uint8_t* dsc = a.down_s + brow * (a.I / 32);
-  v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-  for (int k0 = 0; k0 < a.I; k0 += 128) {
-    const int blk = k0 / 32 + g;
-    uint4 b = *reinterpret_cast<const uint4*>(dw + k0 / 8 + 4 * g);
-    int sb = dsc[blk];
-    v8i A = a_operand(abase, k0, g, avalid);
-    int sa = avalid ? (int)ascl[blk] : 127;
-    acc = MFMA_F8xF4(A, b_operand(b), acc, sa, sb);
-  }
-  float v[4];
+  const int UR = a.Umax * a.R;
+  // the first item's metadata is loaded together with the expert count (one round trip)
+  int nxt_cnt = a.ucnt[min(wave >> 1, a.Umax - 1)], nxt_slot = a.uslot[min(wave >> 1, a.Umax - 1)];
+  const int U = a.n_unique ? min(*a.n_unique, a.Umax) : a.Umax;
+  for (int item = wave; item < 2 * U; item += 16) {
+    const int u = item >> 1, kh = item & 1;
+    const int cnt = min(nxt_cnt, a.R);
+    const int slot = nxt_slot;
+    if (item + 16 < 2 * U) { nxt_cnt = a.ucnt[(item + 16) >> 1]; nxt_slot = a.uslot[(item + 16) >> 1]; }
+    const bool active = cnt > 0 && slot >= 0 && slot < a.S;
+    const bool avalid = active && arow < cnt;
+    const size_t hrow = (size_t)u * a.R + (avalid ? arow : 0);
+    const int b0 = kh * NS * 4;      // first 32-block of this K-half
+    const uint4* xr = reinterpret_cast<const uint4*>((i < 8 ? a.hq_hi : a.hq_lo) + hrow * a.I + b0 * 32) + g;
+    const uint32_t* xs = reinterpret_cast<const uint32_t*>((i < 8 ? a.hq_hs : a.hq_ls) + hrow * (a.I / 32) + b0);
+    const size_t brow = (size_t)(active ? slot : 0) * a.H + m0 + i;
+    const uint4* dw = reinterpret_cast<const uint4*>(a.down_w + brow * (a.I / 8)) + b0 + g;
+    const uint32_t* dsw = reinterpret_cast<const uint32_t*>(a.down_s + brow * (a.I / 32) + b0);
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    {
+      constexpr int PF = NS < 4 ? NS : 4;
+      uint4 bw[NS], xa[PF], xb[PF];
+      uint32_t sbw[NS], saw[PF];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) v[q] = acc[q] + __shfl_xor(acc[q], 32, 64);
-  if (lane < 32) {
-    const int m = m0 + i;
+      for (int s = 0; s < NS; ++s) bw[s] = dw[4 * s];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = 4 * g + q;
-      if (r < cnt) {
-        float d = v[q];
-        if (a.round_bf16) d = round_bf16(d);
-        a.part[((size_t)u * a.R + r) * a.H + m] = d * a.uw[u * a.R + r];
-      } else if (a.zero_pad && r < a.R) {
-        a.part[((size_t)u * a.R + r) * a.H + m] = 0.0f;
+      for (int s = 0; s < NS; ++s) sbw[s] = dsw[s];
+#pragma unroll
+      for (int s = 0; s < PF; ++s) { xa[s] = xr[8 * s]; xb[s] = xr[8 * s + 4]; saw[s] = xs[s]; }
+      __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first MFMA
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const uint4 p = zero_if(xa[s % PF], avalid), q = zero_if(xb[s % PF], avalid);
+        const int sa = avalid ? (int)byte_of(saw[s % PF], g) : 127;
+        if (s + PF < NS) { xa[s % PF] = xr[8 * (s + PF)]; xb[s % PF] = xr[8 * (s + PF) + 4]; saw[s % PF] = xs[s + PF]; }
+        v8i A = {(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, (int)q.z, (int)q.w};
+        acc = MFMA_F8xF4(A, b_operand(bw[s]), acc, sa, (int)byte_of(sbw[s], g));
+      }
+    }
+    float dq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dq[q] = acc[q] + __shfl_xor(acc[q], 32, 64);   // hi rows + lo rows
+    if (lane < 32) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 4 * g + q;
+        if (r < a.R) plds[(kh * UR + u * a.R + r) * 16 + i] = (active && r < cnt) ? dq[q] : 0.0f;
       }
     }
   }
-}
-
-// ------------------------------------------------------------------ fixed-order combine
-// y[row] = bf16(sum_j part[gidx[row*k + j]]), j ascending (kernels.py:198-199).
-__global__ void __launch_bounds__(256) decode_combine_kernel(const float* __restrict__ part, const uint32_t* __restrict__ gidx,
-                                                             int k, int H, uint32_t nrows, uint16_t* __restrict__ y) {
-  const int row = blockIdx.y;
-  const int m = (blockIdx.x * 256 + threadIdx.x) * 4;
-  if (m >= H) return;
-  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int j = 0; j < k; ++j) {
-    const uint32_t idx = gidx[row * k + j];
-    if (idx >= nrows) continue;                  // caller-supplied gather index out of range
-    const float4 p = *reinterpret_cast<const float4*>(part + (size_t)idx * H + m);
-    acc.x = acc.x + p.x;
-    acc.y = acc.y + p.y;
-    acc.z = acc.z + p.z;
-    acc.w = acc.w + p.w;
+  __syncthreads();
+  if (a.zero_pad) {          // copy of the partials (kernels.py:120) for callers that asked for them
+    for (int e = tid; e < U * a.R * 16; e += blockDim.x) {
+      const int row = e >> 4, mi = e & 15;
+      float d = plds[row * 16 + mi] + plds[(UR + row) * 16 + mi];
+      if (a.round_bf16) d = round_bf16(d);
+      a.part[(size_t)row * a.H + m0 + mi] = d * a.uw[row];
+    }
   }
-  uint2 o;
-  o.x = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
-  o.y = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
-  *reinterpret_cast<uint2*>(y + (size_t)row * H + m) = o;
+  const uint32_t nrows = (uint32_t)(U * a.R);
+  for (int e = tid; e < a.M * 16; e += blockDim.x) {
+    const int row = e >> 4, mi = e & 15;
+    float accy = 0.0f;
+    for (int j = 0; j < a.k; ++j) {
+      const uint32_t idx = a.gidx[row * a.k + j];
+      if (idx < nrows) {
+        float d = plds[idx * 16 + mi] + plds[(UR + idx) * 16 + mi];
+        if (a.round_bf16) d = round_bf16(d);
+        accy = accy + d * a.uw[idx];
+      }
+    }
+    a.y[(size_t)row * a.H + m0 + mi] = f32_to_bf16(accy);
+  }
 }
 
 // ------------------------------------------------------------------ host
@@ -250,9 +299,15 @@ static ExpertsWs carve_experts(Carve& c, int M, int Umax, int R, int H, int I) {
 static int check_bank(const mimo_bank* b) {
   MIMO_REQUIRE(b && b->gate_w && b->gate_s && b->up_w && b->up_s && b->down_w && b->down_s, MIMO_ERR_ARG,
                "bank: null pointer");
-  MIMO_REQUIRE(b->n_slots >= 1 && b->hidden >= 256 && b->hidden % 256 == 0 && b->inter >= 128 && b->inter % 128 == 0,
-               MIMO_ERR_SHAPE, "bank: need hidden %% 256 == 0 and inter %% 128 == 0 (got H=%d I=%d)", b->hidden,
-               b->inter);
+  const int H = b->hidden, ns = gateup_steps(H);
+  const int nsd = b->inter / 256;
+  MIMO_REQUIRE(b->n_slots >= 1 && (ns == 1 || ns == 2 || ns == 4 || ns == 8) && H % 256 == 0 && b->inter % 256 == 0 &&
+                   (nsd == 2 || nsd == 4 || nsd == 8),
+               MIMO_ERR_SHAPE, "bank: need hidden in {256, 512, 1024, 2048, 4096} and inter in {512, 1024, 2048} (got "
+               "H=%d I=%d)", b->hidden, b->inter);
+  MIMO_REQUIRE(((reinterpret_cast<uintptr_t>(b->gate_s) | reinterpret_cast<uintptr_t>(b->up_s) |
+                 reinterpret_cast<uintptr_t>(b->down_s)) & 3) == 0,
+               MIMO_ERR_ALIGN, "bank: scale pools must be 4-byte aligned");
   MIMO_REQUIRE(aligned16(b->gate_w) && aligned16(b->up_w) && aligned16(b->down_w), MIMO_ERR_ALIGN,
                "bank: weight pools must be 16-byte aligned");
   return MIMO_OK;
@@ -261,11 +316,26 @@ static int check_bank(const mimo_bank* b) {
 static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream_t st) {
   ExpertsArgs a = base;
   a.round_bf16 = round_bf16;
-  dim3 g1(a.I / 32, a.Umax), g2(a.H / 64, a.Umax), g3((a.H + 1023) / 1024, M);
-  { ProfScope p(st, "decode_gateup"); decode_gateup_kernel<<<g1, 256, 0, st>>>(a); }
-  { ProfScope p(st, "decode_down"); decode_down_kernel<<<g2, 256, 0, st>>>(a); }
-  { ProfScope p(st, "decode_combine");
-    decode_combine_kernel<<<g3, 256, 0, st>>>(a.part, a.gidx, a.k, a.H, (uint32_t)(a.Umax * a.R), a.y); }
+  dim3 g1(a.I / 32, a.Umax);
+  const int ns = gateup_steps(a.H);    // MFMA steps per wave
+  {
+    ProfScope p(st, "decode_gateup");
+    switch (ns) {
+      case 8: decode_gateup_kernel<8><<<g1, 512, 0, st>>>(a); break;
+      case 4: decode_gateup_kernel<4><<<g1, 512, 0, st>>>(a); break;
+      case 2: decode_gateup_kernel<2><<<g1, 512, 0, st>>>(a); break;
+      default: decode_gateup_kernel<1><<<g1, 512, 0, st>>>(a); break;
+    }
+  }
+  const size_t lds = 2 * (size_t)a.Umax * a.R * 16 * sizeof(float);
+  {
+    ProfScope p(st, "decode_down_combine");
+    switch (a.I / 256) {
+      case 8: decode_down_combine_kernel<8><<<a.H / 16, 1024, lds, st>>>(a); break;
+      case 4: decode_down_combine_kernel<4><<<a.H / 16, 1024, lds, st>>>(a); break;
+      default: decode_down_combine_kernel<2><<<a.H / 16, 1024, lds, st>>>(a); break;
+    }
+  }
   return check_launch("moe experts");
 }
 
@@ -288,8 +358,8 @@ int mimo_moe_experts(const uint16_t* x, int M, const mimo_bank* bank, const int3
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && uslot && urows && ucnt && uw && gidx && y, MIMO_ERR_ARG, "moe_experts: null pointer");
-  MIMO_REQUIRE(M >= 1 && M <= 8 && R >= 1 && R <= 8 && k >= 1 && Umax >= 1 && Umax <= M * k, MIMO_ERR_SHAPE,
-               "moe_experts: need 1 <= M <= 8, 1 <= R <= 8, 1 <= Umax <= M*k");
+  MIMO_REQUIRE(M >= 1 && M <= 8 && R >= 1 && R <= 8 && k >= 1 && Umax >= 1 && Umax <= M * k && Umax * R <= 1024,
+               MIMO_ERR_SHAPE, "moe_experts: need 1 <= M <= 8, 1 <= R <= 8, 1 <= Umax <= M*k, Umax*R <= 1024");
   MIMO_REQUIRE(aligned16(x) && aligned16(y) && (!part_out || aligned16(part_out)), MIMO_ERR_ALIGN,
                "moe_experts: x, y, part_out must be 16-byte aligned");
   const int H = bank->hidden, I = bank->inter;
@@ -318,9 +388,8 @@ int mimo_moe_experts(const uint16_t* x, int M, const mimo_bank* bank, const int3
 }
 
 static void carve_decode(Carve& c, int M, int E, int k, int Umax, int R, float** logits, float** scores, float** keys,
-                         int** counter, int32_t** inds, float** w, int32_t** uids, int32_t** urows, int32_t** ucnt,
+                         int32_t** inds, float** w, int32_t** uids, int32_t** urows, int32_t** ucnt,
                          float** uw, uint32_t** gidx, int32_t** nu, int32_t** status) {
-  *counter = c.take<int>(1);
   *logits = c.take<float>((size_t)M * E);
   *scores = c.take<float>((size_t)M * E);
   *keys = c.take<float>((size_t)M * E);
@@ -341,10 +410,9 @@ size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
   Carve c(nullptr, 0);
   int Umax = M * k < E ? M * k : E;
   float *l, *s, *kk, *w, *uw;
-  int* cnt;
   int32_t *inds, *uids, *urows, *ucnt, *nu, *st;
   uint32_t* gidx;
-  carve_decode(c, M, E, k, Umax, kDecodeR, &l, &s, &kk, &cnt, &inds, &w, &uids, &urows, &ucnt, &uw, &gidx, &nu, &st);
+  carve_decode(c, M, E, k, Umax, kDecodeR, &l, &s, &kk, &inds, &w, &uids, &urows, &ucnt, &uw, &gidx, &nu, &st);
   carve_experts(c, M, Umax, kDecodeR, H, I);
   return c.off;
 }
@@ -358,14 +426,14 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
   MIMO_REQUIRE(M >= 1 && M <= 8 && k >= 1 && k <= 8 && E >= k && E <= 1024 && bank->n_slots <= 1024, MIMO_ERR_SHAPE,
                "moe_decode: need 1 <= M <= 8, 1 <= k <= 8, k <= E <= 1024");
   MIMO_REQUIRE(aligned16(x) && aligned16(Wg) && aligned16(y), MIMO_ERR_ALIGN, "moe_decode: 16-byte alignment");
+  MIMO_REQUIRE(bank->hidden <= 4096, MIMO_ERR_SHAPE, "moe_decode: the fused router keeps a row in registers: H <= 4096");
   const int H = bank->hidden, I = bank->inter, S = bank->n_slots;
   const int Umax = M * k < S ? M * k : S;
   Carve c(ws, ws_bytes);
   float *logits, *scores, *keys, *w, *uw;
-  int* counter;
   int32_t *inds, *uids, *urows, *ucnt, *nu, *status;
   uint32_t* gidx;
-  carve_decode(c, M, E, k, Umax, kDecodeR, &logits, &scores, &keys, &counter, &inds, &w, &uids, &urows, &ucnt, &uw,
+  carve_decode(c, M, E, k, Umax, kDecodeR, &logits, &scores, &keys, &inds, &w, &uids, &urows, &ucnt, &uw,
                &gidx, &nu, &status);
   ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_decode: workspace too small (need %zu)", c.off);
@@ -376,7 +444,7 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
 
   RouterSmallArgs ra{};
   ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = M; ra.H = H; ra.E = E; ra.k = k; ra.nlog = (E + 3) / 4;
-  ra.logits = logits; ra.scores = scores; ra.keys = keys; ra.counter = counter;
+  ra.logits = logits; ra.scores = scores; ra.keys = keys;
   ra.inds_out = inds_out ? inds_out : inds;
   ra.w_out = w_out ? w_out : w;
   ra.xq_hi = ew.xq_hi; ra.xq_lo = ew.xq_lo; ra.xq_hs = ew.xq_hs; ra.xq_ls = ew.xq_ls;

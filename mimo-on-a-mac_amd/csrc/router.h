@@ -13,7 +13,6 @@ struct RouterSmallArgs {
   float* logits;           // [T, E]
   float* scores;           // [T, E] sigmoid
   float* keys;             // [T, E] sigmoid + bias
-  int* counter;            // last-block-done counter (zero between launches)
   int32_t* inds_out;       // [T, k] optional
   float* w_out;            // [T, k] optional
   uint8_t *xq_hi, *xq_lo, *xq_hs, *xq_ls;   // optional fp8 split of x: [T, H], [T, H/32]

@@ -17,38 +17,48 @@ namespace mimo {
 __device__ void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,
                                 int32_t* inds_out, float* w_out, int* lds_sel) {
   const int lane = threadIdx.x & 63;
-  // candidates of this lane: e = lane + 64 * j
-  uint64_t cand[16];
+  float* lds_s = reinterpret_cast<float*>(lds_sel + 16);   // lds_sel has room for 32 entries
+  // candidates of this lane: e = lane + 64 * j (ids increase with j), keys and scores loaded in one batch;
+  // value = ordered key + 1 (NaN -> 1), 0 = taken or absent
+  uint32_t cv[16];
+  float sc[16];
   const int per = (E + 63) / 64;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    int e = lane + 64 * j;
-    cand[j] = 0;
-    if (j < per && e < E) cand[j] = ((uint64_t)key_to_ordered(key_row[e]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-    // a NaN key maps to 0 in the high word; the low word (> 0) keeps it selectable, ordered by id
+    const int e = lane + 64 * j;
+    const bool ok = j < per && e < E;
+    const float kv = key_row[ok ? e : 0];
+    sc[j] = s_row[ok ? e : 0];
+    cv[j] = ok ? key_to_ordered(kv) + 1u : 0u;
   }
   for (int r = 0; r < k; ++r) {
-    uint64_t best = 0;
-    int bj = -1;
+    uint32_t bk = 0;
+    int bj = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j)
-      if (cand[j] > best) { best = cand[j]; bj = j; }
-    uint64_t wbest = wave_max_u64(best);
-    if (best == wbest) {                          // exactly one lane owns the maximum (ids are unique)
+      if (cv[j] > bk) { bk = cv[j]; bj = j; }   // first j wins a tie: the lowest id of this lane
+    const uint32_t kmax = dpp_max_u32(bk);
+    const uint32_t myid = (bk == kmax) ? (uint32_t)(lane + 64 * bj) : 0xFFFFFFFFu;
+    const uint32_t idmin = dpp_min_u32(myid);  // ties between lanes go to the lower expert id
+    if (myid == idmin) {
+      float s = 0.0f;
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (j == bj) cand[j] = 0;
+        if (j == bj) { cv[j] = 0; s = sc[j]; }
+      lds_sel[r] = (int)idmin;
+      lds_s[r] = s;
     }
-    if (lane == 0) lds_sel[r] = (int)(0xFFFFFFFFu - (uint32_t)(wbest & 0xFFFFFFFFu));
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   if (lane == 0) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
-    for (int r = 0; r < k; ++r) acc = acc + s_row[lds_sel[r]];
+    for (int r = 0; r < k; ++r) acc = acc + lds_s[r];
     float denom = acc + 1e-20f;
     for (int r = 0; r < k; ++r) {
-      float wv = s_row[lds_sel[r]] / denom;
+      float wv = lds_s[r] / denom;
       if (scaling != 1.0f) wv = wv * scaling;
       inds_out[r] = lds_sel[r];
       w_out[r] = wv;
@@ -113,93 +123,167 @@ __device__ void block_group_routes(const int32_t* inds, const float* scores, con
   if (tid == 0) status[0] = s_bad;
 }
 
+// ------------------------------------------------------------------ grouping (one wave, <= 64 routes)
+// The same outputs as block_group_routes from shuffles only: route t on lane t; lower = earlier routes of its
+// slot (= its row slot c), rank = distinct smaller slots (= u).  lurows/luw: LDS scratch of Umax*R entries.
+__device__ void wave_group_routes(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k,
+                                  int R, int n_slots, int Umax, int32_t* uids, int32_t* urows, int32_t* ucnt,
+                                  float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status, int* lurows,
+                                  float* luw, uint32_t* bits) {
+  const int lane = threadIdx.x & 63;
+  const int nr = M * k;
+  int bad = 0;
+  int s = -1;
+  float sc = 0.0f;
+  if (lane < nr) {
+    int e = inds[lane];
+    s = slot_of ? ((e >= 0) ? slot_of[e] : -1) : e;
+    if (s < 0 || s >= n_slots) { bad = MIMO_ERR_SLOT; s = 0; }
+    sc = scores[lane];
+  }
+  // lanes holding the same slot: AND of per-bit ballots (slot ids < 1024)
+  const uint64_t live = __ballot(lane < nr);
+  uint64_t match = live;
+#pragma unroll
+  for (int b = 0; b < 10; ++b) {
+    const uint64_t m = __ballot((s >> b) & 1);
+    match &= ((s >> b) & 1) ? m : ~m;
+  }
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int lower = __popcll(match & below);       // earlier routes of this slot = the route's row slot c
+  const int same = __popcll(match);
+  const int first = (lane < nr && lower == 0) ? 1 : 0;
+  const int U = __popcll(__ballot(first));
+  // rank of the slot among the distinct slots (= u): bitmap of present slots in LDS
+  if (lane < 32) bits[lane] = 0u;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (first) atomicOr(&bits[s >> 5], 1u << (s & 31));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  int rank = 0;
+  const int sw = s >> 5;
+#pragma unroll
+  for (int w = 0; w < 32; ++w) {
+    const uint32_t bw = bits[w];
+    rank += w < sw ? __popc(bw) : (w == sw ? __popc(bw & ((1u << (s & 31)) - 1u)) : 0);
+  }
+  for (int e = lane; e < Umax * R; e += 64) { lurows[e] = 0; luw[e] = 0.0f; }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (lane < nr) {
+    if (lower >= R) {
+      bad = bad ? bad : MIMO_ERR_ROWS_PER_EXPERT;
+    } else if (rank < Umax) {
+      lurows[rank * R + lower] = lane / k;
+      luw[rank * R + lower] = sc;
+      gidx[lane] = (uint32_t)(rank * R + lower);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  for (int e = lane; e < Umax * R; e += 64) { urows[e] = lurows[e]; uw[e] = luw[e]; }
+  for (int u = lane; u < Umax; u += 64) {
+    ucnt[u] = 0;
+    uids[u] = 0;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  if (first && rank < Umax) {
+    ucnt[rank] = same > R ? R : same;
+    uids[rank] = s;
+  }
+  // most severe code (most negative) over the wave
+  const int worst = -(int)dpp_max_u32((uint32_t)(-bad));
+  if (lane == 0) {
+    n_unique[0] = U;
+    status[0] = worst;
+  }
+}
+
 // ------------------------------------------------------------------ small-T router (T <= 8)
-// Blocks [0, nlog): one wave per expert computes T logits (fp32 FMA over bf16 products), its sigmoid and key.
-// Blocks [nlog, nlog + nquant): fp8 hi/lo split of x (one thread per 32-block) for the expert kernels.
-// The last logits block to finish selects top-k per row (one wave per row) and, if grouping is requested,
-// groups routes by distinct slot.  The done-counter is left at zero.
-__global__ void __launch_bounds__(256) router_small_kernel(RouterSmallArgs a) {
+// Two kernels, no cross-block synchronisation inside either:
+//  router_logits_small_kernel: blocks [0, nlog) give one wave per expert: T logits (fp32 FMA over bf16
+//    products, the expert's weight row loaded in one batch), then sigmoid and key by one lane per row;
+//    blocks [nlog, ...) split x into hi/lo E4M3 halves for the expert kernels (one thread per 32-block).
+//  router_select_group_kernel (one block): top-k per row (one wave per row) and the grouping by slot.
+template <int NCH>
+__global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if ((int)blockIdx.x >= a.nlog) {
+  if ((int)blockIdx.x >= a.nlog) {           // hi/lo split of x: one element per lane, 32 lanes per block
     if (!a.xq_hi) return;
-    int64_t b = (int64_t)(blockIdx.x - a.nlog) * blockDim.x + threadIdx.x;
-    int64_t nb = (int64_t)a.T * (a.H / 32);
-    if (b >= nb) return;
-    const uint4* src = reinterpret_cast<const uint4*>(a.x + b * 32);
-    float v[32];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint4 d = src[c];
-      uint32_t parts[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[c * 8 + 2 * j] = __uint_as_float(parts[j] << 16);
-        v[c * 8 + 2 * j + 1] = __uint_as_float(parts[j] & 0xFFFF0000u);
+    const int64_t n = (int64_t)a.T * a.H;
+    const int64_t idx = ((int64_t)(blockIdx.x - a.nlog) * blockDim.x + threadIdx.x);
+    const bool live = idx < n;
+    const float v = live ? bf16_to_f32(a.x[idx]) : 0.0f;
+    const int X = fp8_block_exp(group_max(fabsf(v), 32));
+    float dec;
+    const uint32_t hc = e4m3_encode(v, X, &dec);
+    const float res = v - dec;
+    const int Y = fp8_block_exp(group_max(fabsf(res), 32));
+    const uint32_t lc = e4m3_encode(res, Y, &dec);
+    if (live) {
+      a.xq_hi[idx] = (uint8_t)hc;
+      a.xq_lo[idx] = (uint8_t)lc;
+      if ((lane & 31) == 0) {
+        a.xq_hs[idx >> 5] = (uint8_t)(X + 127);
+        a.xq_ls[idx >> 5] = (uint8_t)(Y + 127);
       }
     }
-    uint32_t hw[8], lw[8];
-    uint8_t hsb, lsb;
-    quant_block_fp8_hilo(v, hw, lw, &hsb, &lsb);
-    uint4* Hp = reinterpret_cast<uint4*>(a.xq_hi + b * 32);
-    uint4* Lp = reinterpret_cast<uint4*>(a.xq_lo + b * 32);
-    Hp[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    Hp[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    Lp[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    Lp[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-    a.xq_hs[b] = hsb;
-    a.xq_ls[b] = lsb;
     return;
   }
   const int e = blockIdx.x * 4 + wave;
-  if (e < a.E) {
-    float acc[8];
+  if (e >= a.E) return;                          // wave-uniform; no block-level synchronisation below
+  // lane owns the 8-element chunks c*512 + lane*8 (c < NCH); chunks past H read element 0 and count 0
+  const uint16_t* wrow = a.Wg + (size_t)e * a.H;
+  uint4 wq[NCH];
+  bool ok[NCH];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
-    const uint16_t* wrow = a.Wg + (size_t)e * a.H;
-    for (int k0 = lane * 8; k0 < a.H; k0 += 512) {
-      uint4 wq = *reinterpret_cast<const uint4*>(wrow + k0);
-      float wf[8];
-      uint32_t wp[4] = {wq.x, wq.y, wq.z, wq.w};
+  for (int c = 0; c < NCH; ++c) {
+    const int off = c * 512 + lane * 8;
+    ok[c] = off < a.H;
+    wq[c] = *reinterpret_cast<const uint4*>(wrow + (ok[c] ? off : 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float mine = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { wf[2 * j] = __uint_as_float(wp[j] << 16); wf[2 * j + 1] = __uint_as_float(wp[j] & 0xFFFF0000u); }
+  for (int r = 0; r < 8; ++r) {
+    if (r < a.T) {
+      const uint16_t* xrow = a.x + (size_t)r * a.H;
+      uint4 xq[NCH];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        if (r < a.T) {
-          uint4 xq = *reinterpret_cast<const uint4*>(a.x + (size_t)r * a.H + k0);
-          uint32_t xp[4] = {xq.x, xq.y, xq.z, xq.w};
+      for (int c = 0; c < NCH; ++c) xq[c] = *reinterpret_cast<const uint4*>(xrow + (ok[c] ? c * 512 + lane * 8 : 0));
+      float acc = 0.0f;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[r] = fmaf(__uint_as_float(xp[j] << 16), wf[2 * j], acc[r]);
-            acc[r] = fmaf(__uint_as_float(xp[j] & 0xFFFF0000u), wf[2 * j + 1], acc[r]);
-          }
+      for (int c = 0; c < NCH; ++c) {
+        const uint4 xv = ok[c] ? xq[c] : make_uint4(0, 0, 0, 0);
+        uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+        uint32_t wp[4] = {wq[c].x, wq[c].y, wq[c].z, wq[c].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc = fmaf(__uint_as_float(xp[j] << 16), __uint_as_float(wp[j] << 16), acc);
+          acc = fmaf(__uint_as_float(xp[j] & 0xFFFF0000u), __uint_as_float(wp[j] & 0xFFFF0000u), acc);
         }
       }
-    }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      if (r < a.T) {
-        float l = wave_sum(acc[r]);
-        if (lane == 0) {
-          float s = sigmoid_spec(l);
-          a.logits[r * a.E + e] = l;
-          a.scores[r * a.E + e] = s;
-          a.keys[r * a.E + e] = s + a.bias[e];
-        }
-      }
+      float l = wave_sum(acc);
+      if (lane == r) mine = l;
     }
   }
-  // last-block-done
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int old = atomicAdd(a.counter, 1);
-    s_last = (old == a.nlog - 1);
+  if (lane < a.T) {                 // one lane per row: sigmoid and selection key
+    float s = sigmoid_spec(mine);
+    a.logits[lane * a.E + e] = mine;
+    a.scores[lane * a.E + e] = s;
+    a.keys[lane * a.E + e] = s + a.bias[e];
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  __shared__ int sel[4][16];
+}
+
+__global__ void __launch_bounds__(256) router_select_group_kernel(RouterSmallArgs a) {
+  const int wave = threadIdx.x >> 6;
+  __shared__ int sel[4][32];
   __shared__ int32_t s_inds[64];
   __shared__ float s_w[64];
   for (int r = wave; r < a.T; r += 4) {
@@ -210,13 +294,13 @@ __global__ void __launch_bounds__(256) router_small_kernel(RouterSmallArgs a) {
     if (a.inds_out) a.inds_out[i] = s_inds[i];
     if (a.w_out) a.w_out[i] = s_w[i];
   }
-  if (a.uids) {
-    __shared__ int present[1024];
-    __shared__ int route_slot[64];
-    block_group_routes(s_inds, s_w, a.slot_of, a.T, a.k, a.R, a.n_slots, a.Umax, a.uids, a.urows, a.ucnt, a.uw,
-                       a.gidx, a.n_unique, a.status, present, route_slot);
+  if (a.uids && wave == 0) {
+    __shared__ int lurows[512];
+    __shared__ float luw[512];
+    __shared__ uint32_t bits[32];
+    wave_group_routes(s_inds, s_w, a.slot_of, a.T, a.k, a.R, a.n_slots, a.Umax, a.uids, a.urows, a.ucnt, a.uw,
+                      a.gidx, a.n_unique, a.status, lurows, luw, bits);
   }
-  if (threadIdx.x == 0) atomicExch(a.counter, 0);
 }
 
 // ------------------------------------------------------------------ general-T logits: tiled fp32 GEMM
@@ -272,7 +356,7 @@ __global__ void __launch_bounds__(256) router_select_kernel(const float* __restr
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float* s_row = sm + wave * 2 * E;
   float* k_row = s_row + E;
-  __shared__ int sel[4][16];
+  __shared__ int sel[4][32];
   __shared__ int32_t oi[4][16];
   __shared__ float ow[4][16];
   const int t = blockIdx.x * 4 + wave;
@@ -302,6 +386,13 @@ __global__ void group_routes_kernel(const int32_t* inds, const float* scores, co
                                     float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status) {
   __shared__ int present[1024];
   __shared__ int route_slot[1024];
+  __shared__ uint32_t bits[32];
+  if (M * k <= 64 && Umax * R <= 1024) {
+    if (threadIdx.x < 64)
+      wave_group_routes(inds, scores, slot_of, M, k, R, n_slots, Umax, uids, urows, ucnt, uw, gidx, n_unique, status,
+                        present, reinterpret_cast<float*>(route_slot), bits);
+    return;
+  }
   block_group_routes(inds, scores, slot_of, M, k, R, n_slots, Umax, uids, urows, ucnt, uw, gidx, n_unique, status,
                      present, route_slot);
 }
@@ -418,9 +509,21 @@ size_t dispatch_workspace(int n, int n_slots) {
 }
 
 int launch_router_small(const RouterSmallArgs& a, hipStream_t st) {
-  int nquant = a.xq_hi ? (int)(((int64_t)a.T * (a.H / 32) + 255) / 256) : 0;
-  ProfScope p(st, "router_small");
-  router_small_kernel<<<a.nlog + nquant, 256, 0, st>>>(a);
+  int nquant = a.xq_hi ? (int)(((int64_t)a.T * a.H + 255) / 256) : 0;
+  const int nch = (a.H + 511) / 512;
+  {
+    ProfScope p(st, "router_logits_small");
+    switch (nch) {
+      case 8: router_logits_small_kernel<8><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+      case 4: router_logits_small_kernel<4><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+      case 2: router_logits_small_kernel<2><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+      default: router_logits_small_kernel<1><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+    }
+  }
+  {
+    ProfScope p(st, "router_select_group");
+    router_select_group_kernel<<<1, 256, 0, st>>>(a);
+  }
   return check_launch("router_small");
 }
 

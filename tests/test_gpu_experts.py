@@ -1,7 +1,7 @@
 """GPU decode-path parity: distinct-expert kernels (moe_experts), the fused decode block, determinism.
 
 Bars: GPU vs the oracle with the reference's rounding points: max|dy| / max|y| < 1e-2 and >= 99% of elements
-within one bf16 ulp (they differ only where the fp32 accumulation order moves a value across a bf16 rounding
+within two bf16 ulps (they differ only where the fp32 accumulation order moves a value across a bf16 rounding
 boundary: one ulp is 2^-8 relative); GPU vs the reference test's fp32 oracle (engine/tests/test_kernels.py:79):
 < 2e-2; nibble-swapped weights (bench/reports/kernels.md:16): > 0.5."""
 import numpy as np
@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import experts as ox, routing as orr, mxfp4 as oq
-from helpers import assert_bf16_close, bf16_np, pool_np, rand_bf16, to_dev_bf16
+from helpers import assert_bf16_close, bf16_np, pool_np, rand_bf16, shared_routes, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-2
@@ -29,10 +29,8 @@ def tiny_pool():
     return bank, pool_np(bank)
 
 
-def _routes(rng, M, S, k, share=True):
-    inds = np.stack([rng.choice(S, k, replace=False) for _ in range(M)]).astype(np.int32)
-    if M > 1 and share:
-        inds[1, :k // 2] = inds[0, :k // 2]
+def _routes(rng, M, S, k):
+    inds = shared_routes(rng, M, S, k)
     scores = rng.random((M, k)).astype(np.float32)
     scores /= scores.sum(1, keepdims=True)
     return inds, scores
@@ -58,7 +56,7 @@ def test_moe_experts_mimo_shape(rng, mimo_pool, M):
     e_y, f_y = assert_bf16_close(bf16_np(y), oy, what="y")
     e_ref = ox.rel_err(bf16_np(y), ox.reference_fp32(x, pool, inds, scores))
     assert e_ref < 2e-2, e_ref
-    print(f"M={M} U={U} err_vs_oracle h={e_h:.2e} ({f_h:.4f} within 1 ulp) y={e_y:.2e} ({f_y:.4f})  "
+    print(f"M={M} U={U} err_vs_oracle h={e_h:.2e} ({f_h:.4f} within 2 ulps) y={e_y:.2e} ({f_y:.4f})  "
           f"err_vs_fp32_reference={e_ref:.2e}")
 
 
@@ -171,3 +169,19 @@ def test_slot_table_indirection(rng, tiny_pool):
     uids, urows, ucnt, uw, gidx = orr.group_routes(slot_of[gi], gw, R=8)
     oy, _, _ = ox.moe_experts(x, pool, uids, urows, ucnt, uw, gidx, 2, R=8)
     assert_bf16_close(bf16_np(y), oy, what="slot table")
+
+
+def test_workspace_reuse_across_shapes(rng, tiny_pool, mimo_pool):
+    """One cached workspace serves calls of different shapes: the completion counters sit at fixed offsets,
+    so a call after a differently-shaped call still finds them at zero (regression test)."""
+    tbank, tpool = tiny_pool
+    mbank, _ = mimo_pool
+    tblk, _, _ = _block(rng, tbank, 256, 8, 2)
+    mblk, _, _ = _block(rng, mbank, 4096, 24, 8)
+    xt = to_dev_bf16(rand_bf16(rng, (3, 256)))
+    xm = to_dev_bf16(rand_bf16(rng, (8, 4096)))
+    y1 = tblk(xt)
+    for M in (8, 1, 5):
+        mblk(xm[:M])
+    y2 = tblk(xt)
+    assert torch.equal(y1, y2)

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import routing as orr, mxfp4 as oq
-from helpers import to_dev_bf16, zipf_routes
+from helpers import shared_routes, to_dev_bf16, zipf_routes
 
 pytestmark = pytest.mark.gpu
 
@@ -53,9 +53,7 @@ def test_router_logits_and_routes(rng):
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_group_routes_bit_exact(rng, M):
     from mimo_stream import group_routes
-    inds = np.stack([rng.choice(24, 8, replace=False) for _ in range(M)]).astype(np.int32)
-    if M > 1:
-        inds[1, :4] = inds[0, :4]
+    inds = shared_routes(rng, M, 24, 8)
     scores = rng.random((M, 8)).astype(np.float32)
     got = group_routes(inds, scores, R=8, n_slots=24)
     ref = orr.group_routes(inds, scores, R=8)
