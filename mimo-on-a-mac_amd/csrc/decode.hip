@@ -18,6 +18,7 @@
 #include "device.h"
 #include "host.h"
 #include "router.h"
+#include "routing.h"
 
 namespace mimo {
 
@@ -35,6 +36,16 @@ struct ExpertsArgs {
   float* part;                              // [Umax, R, H]
   int round_bf16, zero_pad;
   uint16_t* y;                              // [M, H]
+  // fused decode: the gate/up blocks select and group the routes themselves from the router's scores/keys
+  const float *scores, *keys;               // [M, E]
+  int E;
+  const int32_t* slot_of;                   // [E] expert -> slot, or null (identity)
+  int32_t* inds_out;                        // [M, k] routes (optional)
+  float* w_out;                             // [M, k] weights (optional)
+  int32_t *rt_uids, *rt_urows, *rt_ucnt;    // grouping written by block (0, 0) for the down kernel
+  float* rt_uw;
+  uint32_t* rt_gidx;
+  int32_t *rt_nu, *rt_status;
 };
 
 // A operand (FP8 layout) for K-step k0 from a row of E4M3 codes; zero for padding rows.
@@ -64,16 +75,54 @@ __device__ __forceinline__ uint4 zero_if(uint4 v, bool keep) {
   return keep ? v : make_uint4(0, 0, 0, 0);
 }
 
-template <int NS>
+template <int NS, bool ROUTED>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a) {
   const int u = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
   const int arow = min(i & 7, a.R - 1);
-  // the routing metadata is loaded in one round trip (u < Umax, so every address is valid)
-  const int U = a.n_unique ? *a.n_unique : a.Umax;
-  const int cnt_raw = a.ucnt[u];
-  const int slot = a.uslot[u];
-  int token = a.urows[u * a.R + arow];
+  int U, cnt_raw, slot, token;
+  if (ROUTED) {
+    // routes of this step: wave r selects row r (top-k and renormalisation), wave 0 groups them by slot; every
+    // block does this (it costs less than a separate launch) and block (0, 0) publishes the result
+    __shared__ int sel[8][32];
+    __shared__ int32_t s_inds[64];
+    __shared__ float s_w[64];
+    __shared__ int lurows[512];
+    __shared__ float luw[512];
+    __shared__ uint32_t bits[32];
+    __shared__ int32_t g_uids[64], g_urows[512], g_ucnt[64], g_nu[2];
+    __shared__ float g_uw[512];
+    __shared__ uint32_t g_gidx[64];
+    if (wave < a.M)
+      wave_select_row(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k,
+                      s_w + wave * a.k, sel[wave]);
+    __syncthreads();
+    if (wave == 0)
+      wave_group_routes(s_inds, s_w, a.slot_of, a.M, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
+                        &g_nu[0], &g_nu[1], lurows, luw, bits);
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      const int nr = a.M * a.k;
+      for (int e = tid; e < a.Umax * a.R; e += blockDim.x) { a.rt_urows[e] = g_urows[e]; a.rt_uw[e] = g_uw[e]; }
+      for (int e = tid; e < a.Umax; e += blockDim.x) { a.rt_uids[e] = g_uids[e]; a.rt_ucnt[e] = g_ucnt[e]; }
+      for (int e = tid; e < nr; e += blockDim.x) {
+        a.rt_gidx[e] = g_gidx[e];
+        if (a.inds_out) a.inds_out[e] = s_inds[e];
+        if (a.w_out) a.w_out[e] = s_w[e];
+      }
+      if (tid == 0) { a.rt_nu[0] = g_nu[0]; a.rt_status[0] = g_nu[1]; }
+    }
+    U = g_nu[0];
+    cnt_raw = g_ucnt[u];
+    slot = g_uids[u];
+    token = g_urows[u * a.R + arow];
+  } else {
+    // the routing metadata is loaded in one round trip (u < Umax, so every address is valid)
+    U = a.n_unique ? *a.n_unique : a.Umax;
+    cnt_raw = a.ucnt[u];
+    slot = a.uslot[u];
+    token = a.urows[u * a.R + arow];
+  }
   if (u >= U) return;
   const int cnt = min(cnt_raw, a.R);
   if (cnt <= 0 || slot < 0 || slot >= a.S) return;     // caller-supplied ids are range-checked
@@ -318,13 +367,27 @@ static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream
   a.round_bf16 = round_bf16;
   dim3 g1(a.I / 32, a.Umax);
   const int ns = gateup_steps(a.H);    // MFMA steps per wave
+  if (a.scores && a.Umax > 16) {
+    int rc = launch_select_group(a.scores, a.keys, a.M, a.E, a.k, a.slot_of, a.R, a.S, a.Umax, a.inds_out, a.w_out,
+                                 a.rt_uids, a.rt_urows, a.rt_ucnt, a.rt_uw, a.rt_gidx, a.rt_nu, a.rt_status, st);
+    if (rc) return rc;
+  }
   {
     ProfScope p(st, "decode_gateup");
-    switch (ns) {
-      case 8: decode_gateup_kernel<8><<<g1, 512, 0, st>>>(a); break;
-      case 4: decode_gateup_kernel<4><<<g1, 512, 0, st>>>(a); break;
-      case 2: decode_gateup_kernel<2><<<g1, 512, 0, st>>>(a); break;
-      default: decode_gateup_kernel<1><<<g1, 512, 0, st>>>(a); break;
+    if (a.scores && a.Umax <= 16) {   // small batches: every block selects (cheaper than a launch)
+      switch (ns) {
+        case 8: decode_gateup_kernel<8, true><<<g1, 512, 0, st>>>(a); break;
+        case 4: decode_gateup_kernel<4, true><<<g1, 512, 0, st>>>(a); break;
+        case 2: decode_gateup_kernel<2, true><<<g1, 512, 0, st>>>(a); break;
+        default: decode_gateup_kernel<1, true><<<g1, 512, 0, st>>>(a); break;
+      }
+    } else {
+      switch (ns) {
+        case 8: decode_gateup_kernel<8, false><<<g1, 512, 0, st>>>(a); break;
+        case 4: decode_gateup_kernel<4, false><<<g1, 512, 0, st>>>(a); break;
+        case 2: decode_gateup_kernel<2, false><<<g1, 512, 0, st>>>(a); break;
+        default: decode_gateup_kernel<1, false><<<g1, 512, 0, st>>>(a); break;
+      }
     }
   }
   const size_t lds = 2 * (size_t)a.Umax * a.R * 16 * sizeof(float);
@@ -445,12 +508,8 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
   RouterSmallArgs ra{};
   ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = M; ra.H = H; ra.E = E; ra.k = k; ra.nlog = (E + 3) / 4;
   ra.logits = logits; ra.scores = scores; ra.keys = keys;
-  ra.inds_out = inds_out ? inds_out : inds;
-  ra.w_out = w_out ? w_out : w;
   ra.xq_hi = ew.xq_hi; ra.xq_lo = ew.xq_lo; ra.xq_hs = ew.xq_hs; ra.xq_ls = ew.xq_ls;
-  ra.slot_of = slot_of; ra.R = kDecodeR; ra.n_slots = S; ra.Umax = Umax;
-  ra.uids = uids; ra.urows = urows; ra.ucnt = ucnt; ra.uw = uw; ra.gidx = gidx; ra.n_unique = nu; ra.status = status;
-  rc = launch_router_small(ra, st);
+  rc = launch_router_logits_small(ra, st);
   if (rc) return rc;
 
   ExpertsArgs a{};
@@ -462,6 +521,11 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
   a.sigtab = sig;
   a.h = ew.h; a.hq_hi = ew.hq_hi; a.hq_lo = ew.hq_lo; a.hq_hs = ew.hq_hs; a.hq_ls = ew.hq_ls;
   a.part = ew.part; a.zero_pad = 0; a.y = y;
+  a.scores = scores; a.keys = keys; a.E = E; a.slot_of = slot_of;
+  a.inds_out = inds_out ? inds_out : inds;
+  a.w_out = w_out ? w_out : w;
+  a.rt_uids = uids; a.rt_urows = urows; a.rt_ucnt = ucnt; a.rt_uw = uw; a.rt_gidx = gidx; a.rt_nu = nu;
+  a.rt_status = status;
   // M == 1 follows _gather_m1 (bf16 expert outputs, model.py:173-182); M >= 2 the distinct-expert kernels
   return run_experts(a, M, M == 1 ? 1 : 0, st);
 }

@@ -13,19 +13,28 @@ struct RouterSmallArgs {
   float* logits;           // [T, E]
   float* scores;           // [T, E] sigmoid
   float* keys;             // [T, E] sigmoid + bias
-  int32_t* inds_out;       // [T, k] optional
-  float* w_out;            // [T, k] optional
   uint8_t *xq_hi, *xq_lo, *xq_hs, *xq_ls;   // optional fp8 split of x: [T, H], [T, H/32]
-  // optional grouping (uids == nullptr: skip)
+};
+
+int launch_router_logits_small(const RouterSmallArgs& a, hipStream_t st);   // logits, sigmoid, keys, x split
+
+struct SelectGroupArgs {
+  const float *scores, *keys;   // [T, E]
+  int T, E, k;
   const int32_t* slot_of;
   int R, n_slots, Umax;
+  int32_t* inds_out;
+  float* w_out;
   int32_t *uids, *urows, *ucnt;
   float* uw;
   uint32_t* gidx;
   int32_t *n_unique, *status;
 };
-
-int launch_router_small(const RouterSmallArgs& a, hipStream_t st);
+// top-k + renormalisation per row and grouping by slot (one block; T <= 8, T*k <= 64, Umax*R <= 512)
+int launch_select_group(const float* scores, const float* keys, int T, int E, int k, const int32_t* slot_of, int R,
+                        int n_slots, int Umax, int32_t* inds_out, float* w_out, int32_t* uids, int32_t* urows,
+                        int32_t* ucnt, float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status,
+                        hipStream_t st);
 int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st);
 int launch_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling, int32_t* inds,
                          float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,

@@ -9,63 +9,9 @@
 #include "device.h"
 #include "host.h"
 #include "router.h"
+#include "routing.h"
 
 namespace mimo {
-
-// ------------------------------------------------------------------ selection (one wave per row)
-// keys/scores for row r live in s_row/key_row (global or LDS); writes k (index, weight) pairs.
-__device__ void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,
-                                int32_t* inds_out, float* w_out, int* lds_sel) {
-  const int lane = threadIdx.x & 63;
-  float* lds_s = reinterpret_cast<float*>(lds_sel + 16);   // lds_sel has room for 32 entries
-  // candidates of this lane: e = lane + 64 * j (ids increase with j), keys and scores loaded in one batch;
-  // value = ordered key + 1 (NaN -> 1), 0 = taken or absent
-  uint32_t cv[16];
-  float sc[16];
-  const int per = (E + 63) / 64;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int e = lane + 64 * j;
-    const bool ok = j < per && e < E;
-    const float kv = key_row[ok ? e : 0];
-    sc[j] = s_row[ok ? e : 0];
-    cv[j] = ok ? key_to_ordered(kv) + 1u : 0u;
-  }
-  for (int r = 0; r < k; ++r) {
-    uint32_t bk = 0;
-    int bj = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (cv[j] > bk) { bk = cv[j]; bj = j; }   // first j wins a tie: the lowest id of this lane
-    const uint32_t kmax = dpp_max_u32(bk);
-    const uint32_t myid = (bk == kmax) ? (uint32_t)(lane + 64 * bj) : 0xFFFFFFFFu;
-    const uint32_t idmin = dpp_min_u32(myid);  // ties between lanes go to the lower expert id
-    if (myid == idmin) {
-      float s = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (j == bj) { cv[j] = 0; s = sc[j]; }
-      lds_sel[r] = (int)idmin;
-      lds_s[r] = s;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  if (lane == 0) {
-#pragma clang fp contract(off)
-    float acc = 0.0f;
-    for (int r = 0; r < k; ++r) acc = acc + lds_s[r];
-    float denom = acc + 1e-20f;
-    for (int r = 0; r < k; ++r) {
-      float wv = lds_s[r] / denom;
-      if (scaling != 1.0f) wv = wv * scaling;
-      inds_out[r] = lds_sel[r];
-      w_out[r] = wv;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-}
 
 // ------------------------------------------------------------------ grouping (one block, <= 1024 routes)
 // group_routes restated: uids ascending, urows/uw in route order per expert, gidx = u*R + c.
@@ -121,88 +67,6 @@ __device__ void block_group_routes(const int32_t* inds, const float* scores, con
   if (bad) atomicMin(&s_bad, bad);      // codes are negative: min = most severe, order independent
   __syncthreads();
   if (tid == 0) status[0] = s_bad;
-}
-
-// ------------------------------------------------------------------ grouping (one wave, <= 64 routes)
-// The same outputs as block_group_routes from shuffles only: route t on lane t; lower = earlier routes of its
-// slot (= its row slot c), rank = distinct smaller slots (= u).  lurows/luw: LDS scratch of Umax*R entries.
-__device__ void wave_group_routes(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k,
-                                  int R, int n_slots, int Umax, int32_t* uids, int32_t* urows, int32_t* ucnt,
-                                  float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status, int* lurows,
-                                  float* luw, uint32_t* bits) {
-  const int lane = threadIdx.x & 63;
-  const int nr = M * k;
-  int bad = 0;
-  int s = -1;
-  float sc = 0.0f;
-  if (lane < nr) {
-    int e = inds[lane];
-    s = slot_of ? ((e >= 0) ? slot_of[e] : -1) : e;
-    if (s < 0 || s >= n_slots) { bad = MIMO_ERR_SLOT; s = 0; }
-    sc = scores[lane];
-  }
-  // lanes holding the same slot: AND of per-bit ballots (slot ids < 1024)
-  const uint64_t live = __ballot(lane < nr);
-  uint64_t match = live;
-#pragma unroll
-  for (int b = 0; b < 10; ++b) {
-    const uint64_t m = __ballot((s >> b) & 1);
-    match &= ((s >> b) & 1) ? m : ~m;
-  }
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  const int lower = __popcll(match & below);       // earlier routes of this slot = the route's row slot c
-  const int same = __popcll(match);
-  const int first = (lane < nr && lower == 0) ? 1 : 0;
-  const int U = __popcll(__ballot(first));
-  // rank of the slot among the distinct slots (= u): bitmap of present slots in LDS
-  if (lane < 32) bits[lane] = 0u;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  if (first) atomicOr(&bits[s >> 5], 1u << (s & 31));
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  int rank = 0;
-  const int sw = s >> 5;
-#pragma unroll
-  for (int w = 0; w < 32; ++w) {
-    const uint32_t bw = bits[w];
-    rank += w < sw ? __popc(bw) : (w == sw ? __popc(bw & ((1u << (s & 31)) - 1u)) : 0);
-  }
-  for (int e = lane; e < Umax * R; e += 64) { lurows[e] = 0; luw[e] = 0.0f; }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  if (lane < nr) {
-    if (lower >= R) {
-      bad = bad ? bad : MIMO_ERR_ROWS_PER_EXPERT;
-    } else if (rank < Umax) {
-      lurows[rank * R + lower] = lane / k;
-      luw[rank * R + lower] = sc;
-      gidx[lane] = (uint32_t)(rank * R + lower);
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  for (int e = lane; e < Umax * R; e += 64) { urows[e] = lurows[e]; uw[e] = luw[e]; }
-  for (int u = lane; u < Umax; u += 64) {
-    ucnt[u] = 0;
-    uids[u] = 0;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  if (first && rank < Umax) {
-    ucnt[rank] = same > R ? R : same;
-    uids[rank] = s;
-  }
-  // most severe code (most negative) over the wave
-  const int worst = -(int)dpp_max_u32((uint32_t)(-bad));
-  if (lane == 0) {
-    n_unique[0] = U;
-    status[0] = worst;
-  }
 }
 
 // ------------------------------------------------------------------ small-T router (T <= 8)
@@ -281,26 +145,37 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
   }
 }
 
-__global__ void __launch_bounds__(256) router_select_group_kernel(RouterSmallArgs a) {
+// One block, one wave per row: top-k and renormalisation, then wave 0 groups the routes by slot.
+__global__ void __launch_bounds__(512) router_select_group_kernel(SelectGroupArgs a) {
   const int wave = threadIdx.x >> 6;
-  __shared__ int sel[4][32];
+  __shared__ int sel[8][32];
   __shared__ int32_t s_inds[64];
   __shared__ float s_w[64];
-  for (int r = wave; r < a.T; r += 4) {
-    wave_select_row(a.scores + r * a.E, a.keys + r * a.E, a.E, a.k, 1.0f, s_inds + r * a.k, s_w + r * a.k, sel[wave]);
-  }
+  __shared__ int lurows[512];
+  __shared__ float luw[512];
+  __shared__ uint32_t bits[32];
+  if (wave < a.T)
+    wave_select_row(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k, s_w + wave * a.k,
+                    sel[wave]);
   __syncthreads();
   for (int i = threadIdx.x; i < a.T * a.k; i += blockDim.x) {
     if (a.inds_out) a.inds_out[i] = s_inds[i];
     if (a.w_out) a.w_out[i] = s_w[i];
   }
-  if (a.uids && wave == 0) {
-    __shared__ int lurows[512];
-    __shared__ float luw[512];
-    __shared__ uint32_t bits[32];
+  if (wave == 0)
     wave_group_routes(s_inds, s_w, a.slot_of, a.T, a.k, a.R, a.n_slots, a.Umax, a.uids, a.urows, a.ucnt, a.uw,
                       a.gidx, a.n_unique, a.status, lurows, luw, bits);
-  }
+}
+
+int launch_select_group(const float* scores, const float* keys, int T, int E, int k, const int32_t* slot_of, int R,
+                        int n_slots, int Umax, int32_t* inds_out, float* w_out, int32_t* uids, int32_t* urows,
+                        int32_t* ucnt, float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status,
+                        hipStream_t st) {
+  SelectGroupArgs a{scores, keys, T, E, k, slot_of, R, n_slots, Umax, inds_out, w_out, uids, urows, ucnt, uw, gidx,
+                    n_unique, status};
+  ProfScope p(st, "router_select_group");
+  router_select_group_kernel<<<1, 512, 0, st>>>(a);
+  return check_launch("router_select_group");
 }
 
 // ------------------------------------------------------------------ general-T logits: tiled fp32 GEMM
@@ -508,23 +383,17 @@ size_t dispatch_workspace(int n, int n_slots) {
   return align256((size_t)nchunks * n_slots * sizeof(int32_t));
 }
 
-int launch_router_small(const RouterSmallArgs& a, hipStream_t st) {
+int launch_router_logits_small(const RouterSmallArgs& a, hipStream_t st) {
   int nquant = a.xq_hi ? (int)(((int64_t)a.T * a.H + 255) / 256) : 0;
   const int nch = (a.H + 511) / 512;
-  {
-    ProfScope p(st, "router_logits_small");
-    switch (nch) {
-      case 8: router_logits_small_kernel<8><<<a.nlog + nquant, 256, 0, st>>>(a); break;
-      case 4: router_logits_small_kernel<4><<<a.nlog + nquant, 256, 0, st>>>(a); break;
-      case 2: router_logits_small_kernel<2><<<a.nlog + nquant, 256, 0, st>>>(a); break;
-      default: router_logits_small_kernel<1><<<a.nlog + nquant, 256, 0, st>>>(a); break;
-    }
+  ProfScope p(st, "router_logits_small");
+  switch (nch) {
+    case 8: router_logits_small_kernel<8><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+    case 4: router_logits_small_kernel<4><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+    case 2: router_logits_small_kernel<2><<<a.nlog + nquant, 256, 0, st>>>(a); break;
+    default: router_logits_small_kernel<1><<<a.nlog + nquant, 256, 0, st>>>(a); break;
   }
-  {
-    ProfScope p(st, "router_select_group");
-    router_select_group_kernel<<<1, 256, 0, st>>>(a);
-  }
-  return check_launch("router_small");
+  return check_launch("router_logits_small");
 }
 
 int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st) {
