@@ -30,7 +30,6 @@ struct ExpertsArgs {
   const int32_t *uslot, *urows, *ucnt, *n_unique;
   const float* uw;
   const uint32_t* gidx;
-  const uint16_t* sigtab;
   uint16_t* h;                              // [Umax, R, I] bf16
   uint8_t *hq_hi, *hq_lo, *hq_hs, *hq_ls;   // [Umax, R, I], [Umax, R, I/32]
   float* part;                              // [Umax, R, H]
@@ -61,12 +60,14 @@ __device__ __forceinline__ v8i b_operand(uint4 b) { return v8i{(int)b.x, (int)b.
 
 // ------------------------------------------------------------------ Kernel A: gate/up + SwiGLU
 // Block (512 threads): one distinct expert u (blockIdx.y) x 32 outputs n (blockIdx.x).  Wave w: 16-output
-// tile (w & 1) x K-range (w >> 1) of 4.  A wave's K-range is NS MFMA steps of K = 128; all of its loads (16 B
-// of gate and of up weights per lane and step, the activation halves and the scale words) are issued in one
-// straight-line batch before the first MFMA, so a block keeps 8 x 16 KB of expert weights in flight.  Loads
-// never depend on the lane: padding rows read row 0 and are zeroed by selects.  K-range partials are summed
-// in a fixed order through LDS; the epilogue applies the bf16 rounding points of kernels.py:79-82 and writes
-// h and its hi/lo split.
+// tile (w & 1) x K-range (w >> 1) of 4.  A wave's K-range is NS MFMA steps of K = 128 and its 2 x NS weight
+// loads (16 B of gate and of up per lane and step) are issued in one straight-line batch and stay in
+// registers, so a block keeps 8 x 16 KB of expert weights in flight.  Everything else the block reads is
+// requested before that batch: the expert's activation rows go straight to LDS (global_load_lds) and the
+// block's weight scales come in with one or two coalesced loads per thread; a load issued after the weight
+// batch would queue behind it.  Loads never depend on the lane: padding rows read row 0 and are zeroed by
+// selects.  K-range partials are summed in a fixed order through LDS; the epilogue applies the bf16 rounding
+// points of kernels.py:79-82 and writes the hi/lo split of h (and h itself when the caller asked for it).
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int g) { return (w >> (8 * g)) & 0xFFu; }
 // K split of the gate/up reduction: 4 ranges when H % 512 == 0, else 2; MFMA steps (K = 128) per range.
 __host__ __device__ inline int gateup_ksplit(int H) { return H % 512 == 0 ? 4 : 2; }
@@ -74,98 +75,201 @@ __host__ __device__ inline int gateup_steps(int H) { return H / gateup_ksplit(H)
 __device__ __forceinline__ uint4 zero_if(uint4 v, bool keep) {
   return keep ? v : make_uint4(0, 0, 0, 0);
 }
+__host__ __device__ constexpr int align_up(int x, int a) { return (x + a - 1) / a * a; }
+
+// Dynamic LDS of the gate/up kernel (bytes), for hidden size H and `rl` staged activation rows:
+//   scales  2 x 32 rows x RS       gate then up scales of the block's rows, RS = H/32 + 16 (conflict-free reads)
+//   a_hi    rl rows x RA           hi E4M3 codes of the staged rows, RA = H + 16 (rows 4 banks apart)
+//   a_lo    rl rows x RA           lo codes, starting 128 bytes off a_hi's bank phase
+//   a_sc    rl rows x 2 x H/32     [hi scales | lo scales] per row
+// The K-range partials and the h tile reuse the activation region once the MFMA loop is done.
+struct GateupLds {
+  int RS, RA, a_hi, a_lo, a_sc, red, hl, total;
+};
+constexpr int kRedBytes = 4 * 2 * 2 * 32 * 4 * 4;   // [K-range][ntile][gate/up][lane][q] floats
+__host__ __device__ inline GateupLds gateup_lds(int H, int rl) {
+  GateupLds L;
+  L.RS = H / 32 + 16;
+  L.RA = H + 16;
+  L.a_hi = 2 * 32 * L.RS;
+  L.a_lo = align_up(L.a_hi + rl * L.RA, 256) + 128;
+  L.a_sc = align_up(L.a_lo + rl * L.RA, 16);
+  L.red = L.a_hi;
+  L.hl = L.red + kRedBytes;
+  const int a_end = L.a_sc + rl * 2 * (H / 32);
+  const int e_end = L.hl + 8 * 32 * 4;
+  L.total = a_end > e_end ? a_end : e_end;
+  return L;
+}
+
+// Stage activation rows c0 .. c0 + n - 1 of the block's expert into LDS (rows 0 .. n - 1 there): per row, the
+// hi and lo codes in 1 KB pieces and the [hi | lo] scales in one piece, spread over the block's 8 waves,
+// at most JMAX pieces per wave (n <= 8 rows of H <= 4096 need 9).  Straight-line code: a loop here would
+// make the compiler drain every outstanding load before entering it.
+// tok: lane c holds the token of row c (wave-uniform reads through readlane).
+template <int JMAX>
+__device__ __forceinline__ void stage_act_rows(const ExpertsArgs& a, uint8_t* lds, const GateupLds& L, int c0, int n,
+                                               int tok, int wave, int lane) {
+  const int nq = (a.H + 1023) >> 10;          // 1 KB pieces per half row
+  const int per_row = 2 * nq + 1;
+  const int hs = a.H / 32;
+#pragma unroll
+  for (int j = 0; j < JMAX; ++j) {
+    const int t = wave + 8 * j;
+    if (t >= n * per_row) break;
+    const int c = t / per_row, p = t - c * per_row;
+    int token = __builtin_amdgcn_readlane(tok, c0 + c);
+    token = (token < 0 || token >= a.M) ? 0 : token;
+    if (p < 2 * nq) {
+      const int half = p >= nq, q = half ? p - nq : p;
+      const uint8_t* src = (half ? a.xq_lo : a.xq_hi) + (size_t)token * a.H + 1024 * q;
+      const uint8_t* dst = lds + (half ? L.a_lo : L.a_hi) + c * L.RA + 1024 * q;
+      if (1024 * q + 16 * lane < a.H) lds_copy16(src, 16 * lane, dst);
+    } else {                                      // [hi scales | lo scales] of the row, 4 bytes per lane
+      const uint8_t* dst = lds + L.a_sc + c * 2 * hs;
+      if (4 * lane < hs) lds_copy4(a.xq_hs + (size_t)token * hs, 4 * lane, dst);
+      else if (4 * lane < 2 * hs) lds_copy4(a.xq_ls + (size_t)token * hs - hs, 4 * lane, dst);
+    }
+  }
+}
+
+// Block (0, 0) of the routed gate/up kernel writes the step's routes and grouping for the down kernel (and the
+// caller's inds/w), after its own loads: stores ahead of the weight loads would make them wait.
+__device__ __forceinline__ void publish_routes(const ExpertsArgs& a, const int32_t* s_inds, const float* s_w,
+                                               const int32_t* g_uids, const int32_t* g_urows, const int32_t* g_ucnt,
+                                               const float* g_uw, const uint32_t* g_gidx, const int32_t* g_nu, int tid) {
+  if (blockIdx.x != 0 || blockIdx.y != 0) return;
+  const int nr = a.M * a.k;
+  for (int e = tid; e < a.Umax * a.R; e += blockDim.x) { a.rt_urows[e] = g_urows[e]; a.rt_uw[e] = g_uw[e]; }
+  for (int e = tid; e < a.Umax; e += blockDim.x) { a.rt_uids[e] = g_uids[e]; a.rt_ucnt[e] = g_ucnt[e]; }
+  for (int e = tid; e < nr; e += blockDim.x) {
+    a.rt_gidx[e] = g_gidx[e];
+    if (a.inds_out) a.inds_out[e] = s_inds[e];
+    if (a.w_out) a.w_out[e] = s_w[e];
+  }
+  if (tid == 0) { a.rt_nu[0] = g_nu[0]; a.rt_status[0] = g_nu[1]; }
+}
 
 template <int NS, bool ROUTED>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a) {
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a, int rl) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  // routed grouping (ROUTED only): kept for the publication at the end of block (0, 0)
+  __shared__ int sel[ROUTED ? 8 : 1][kSelLds];
+  __shared__ int32_t s_inds[ROUTED ? 64 : 1];
+  __shared__ float s_w[ROUTED ? 64 : 1];
+  __shared__ int lurows[ROUTED ? 512 : 1];
+  __shared__ float luw[ROUTED ? 512 : 1];
+  __shared__ int32_t g_uids[ROUTED ? 64 : 1], g_urows[ROUTED ? 512 : 1], g_ucnt[ROUTED ? 64 : 1], g_nu[2];
+  __shared__ float g_uw[ROUTED ? 512 : 1];
+  __shared__ uint32_t g_gidx[ROUTED ? 64 : 1];
   const int u = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
-  const int arow = min(i & 7, a.R - 1);
-  int U, cnt_raw, slot, token;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar registers)
+  int U, cnt_raw, slot, tok;          // tok: lane c < R holds the token of the expert's row c
   if (ROUTED) {
     // routes of this step: wave r selects row r (top-k and renormalisation), wave 0 groups them by slot; every
-    // block does this (it costs less than a separate launch) and block (0, 0) publishes the result
-    __shared__ int sel[8][32];
-    __shared__ int32_t s_inds[64];
-    __shared__ float s_w[64];
-    __shared__ int lurows[512];
-    __shared__ float luw[512];
-    __shared__ uint32_t bits[32];
-    __shared__ int32_t g_uids[64], g_urows[512], g_ucnt[64], g_nu[2];
-    __shared__ float g_uw[512];
-    __shared__ uint32_t g_gidx[64];
+    // block does this (it costs less than a separate launch) and block (0, 0) publishes the result at its end
     if (wave < a.M)
-      wave_select_row(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k,
-                      s_w + wave * a.k, sel[wave]);
+      wave_select_row_t<4>(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k,
+                           s_w + wave * a.k, sel[wave]);     // E <= 256 on this path
     __syncthreads();
     if (wave == 0)
       wave_group_routes(s_inds, s_w, a.slot_of, a.M, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
-                        &g_nu[0], &g_nu[1], lurows, luw, bits);
+                        &g_nu[0], &g_nu[1], lurows, luw);
     __syncthreads();
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-      const int nr = a.M * a.k;
-      for (int e = tid; e < a.Umax * a.R; e += blockDim.x) { a.rt_urows[e] = g_urows[e]; a.rt_uw[e] = g_uw[e]; }
-      for (int e = tid; e < a.Umax; e += blockDim.x) { a.rt_uids[e] = g_uids[e]; a.rt_ucnt[e] = g_ucnt[e]; }
-      for (int e = tid; e < nr; e += blockDim.x) {
-        a.rt_gidx[e] = g_gidx[e];
-        if (a.inds_out) a.inds_out[e] = s_inds[e];
-        if (a.w_out) a.w_out[e] = s_w[e];
-      }
-      if (tid == 0) { a.rt_nu[0] = g_nu[0]; a.rt_status[0] = g_nu[1]; }
-    }
     U = g_nu[0];
     cnt_raw = g_ucnt[u];
     slot = g_uids[u];
-    token = g_urows[u * a.R + arow];
+    tok = g_urows[u * a.R + min(lane, a.R - 1)];
   } else {
     // the routing metadata is loaded in one round trip (u < Umax, so every address is valid)
     U = a.n_unique ? *a.n_unique : a.Umax;
     cnt_raw = a.ucnt[u];
     slot = a.uslot[u];
-    token = a.urows[u * a.R + arow];
+    tok = a.urows[u * a.R + min(lane, a.R - 1)];
   }
-  if (u >= U) return;
   const int cnt = min(cnt_raw, a.R);
-  if (cnt <= 0 || slot < 0 || slot >= a.S) return;     // caller-supplied ids are range-checked
+  // caller-supplied ids are range-checked; block (0, 0) of the routed kernel never returns here (expert 0 has a
+  // row and a valid slot: the grouping maps invalid slots to 0 and flags them in the status)
+  if (u >= U || cnt <= 0 || slot < 0 || slot >= a.S) return;
+  wait_vm_all();   // the metadata loads are done; nothing the compiler tracks stays in flight past this point
+  const GateupLds L = gateup_lds(a.H, rl);
+  // the activation rows go first (they need only the metadata the weight addresses need as well)
+  constexpr int JMAX = ROUTED ? 3 : 9;    // routed batches stage at most 2 rows at once, others 8
+  stage_act_rows<JMAX>(a, lds, L, 0, min(cnt, rl), tok, wave, lane);
+  __builtin_amdgcn_sched_barrier(0);
+
   const int ntile = wave & 1, kr = wave >> 1;
   const int nb = blockIdx.x * 32;
   const int n0 = nb + ntile * 16;
-  const bool avalid = (i & 7) < cnt;
-  token = (!avalid || token < 0 || token >= a.M) ? 0 : token;
-  const uint8_t* abase = (i < 8 ? a.xq_hi : a.xq_lo) + (size_t)token * a.H;
-  const uint8_t* ascl = (i < 8 ? a.xq_hs : a.xq_ls) + (size_t)token * (a.H / 32);
   const size_t brow = (size_t)slot * a.I + n0 + i;
-  const bool kactive = kr < gateup_ksplit(a.H);     // wave-uniform
-  const int k0 = (kactive ? kr : 0) * NS * 128;
+  const int ksplit = gateup_ksplit(a.H);
+  // with only two K-ranges (small H) waves 4-7 repeat K-range 0 and their partials are not used
+  const int k0 = (kr < ksplit ? kr : 0) * NS * 128;
   const int b0 = k0 / 32;
   const uint4* gw = reinterpret_cast<const uint4*>(a.gate_w + brow * (a.H / 8)) + b0 + g;   // one uint4 per 32-block
   const uint4* upw = reinterpret_cast<const uint4*>(a.up_w + brow * (a.H / 8)) + b0 + g;
-  const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.gate_s + brow * (a.H / 32) + b0);
-  const uint32_t* us = reinterpret_cast<const uint32_t*>(a.up_s + brow * (a.H / 32) + b0);
-  const uint4* xr = reinterpret_cast<const uint4*>(abase + k0) + g;        // 16-byte units
-  const uint32_t* xs = reinterpret_cast<const uint32_t*>(ascl + b0);
+  // the block's gate and up scales (32 rows x H/32 bytes each, contiguous in the pools) in 8-byte pieces
+  const int lg_pr = __builtin_ctz(a.H / 256);             // pieces per scale row = H / 256
+  const int npieces = 64 << lg_pr;
+  const int p0 = tid, p1 = tid + 512;
+  const int q0 = p0 < npieces ? p0 : 0, q1 = p1 < npieces ? p1 : 0;
+  auto piece_src = [&](int p) {
+    const int proj = p >> (5 + lg_pr), row = (p >> lg_pr) & 31, c = p & ((1 << lg_pr) - 1);
+    return reinterpret_cast<const uint2*>((proj ? a.up_s : a.gate_s) + ((size_t)slot * a.I + nb + row) * (a.H / 32)) + c;
+  };
+  auto piece_dst = [&](int p) {
+    const int proj = p >> (5 + lg_pr), row = (p >> lg_pr) & 31, c = p & ((1 << lg_pr) - 1);
+    return reinterpret_cast<uint2*>(lds + (proj * 32 + row) * L.RS + 8 * c);
+  };
+  uint4 bg[NS], bu[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) { bg[s] = gw[4 * s]; bu[s] = upw[4 * s]; }
+  const uint2 sp0 = *piece_src(q0);
+  const uint2 sp1 = *piece_src(q1);
+  __builtin_amdgcn_sched_barrier(0);
+  if (p0 < npieces) *piece_dst(p0) = sp0;
+  if (p1 < npieces) *piece_dst(p1) = sp1;
+  wait_vm_all();
+  __syncthreads();
+
   v4f accg = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (kactive) {
-    // weights (the HBM stream) for every step stay in registers; activations (L2-resident) are loaded
-    // PF steps ahead of their MFMA
-    constexpr int PF = NS < 4 ? NS : 4;
-    uint4 bg[NS], bu[NS], xa[PF], xb[PF];
-    uint32_t sgw[NS], suw[NS], saw[PF];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) { bg[s] = gw[4 * s]; bu[s] = upw[4 * s]; }
-#pragma unroll
-    for (int s = 0; s < NS; ++s) { sgw[s] = gs[s]; suw[s] = us[s]; }
-#pragma unroll
-    for (int s = 0; s < PF; ++s) { xa[s] = xr[8 * s]; xb[s] = xr[8 * s + 4]; saw[s] = xs[s]; }
-    __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first MFMA
+  const uint8_t* lrow = lds + (ntile * 16 + i) * L.RS + b0;   // this lane's gate scale row (up: + 32 rows)
+  const int crow = i & 7;              // the expert's row c carried by this lane (hi rows 0-7, lo rows 8-15)
+  // one pass over the staged rows: the operands of step s + 1 are read from LDS while step s multiplies
+  auto run_pass = [&](int c0) {
+    const bool avalid = crow >= c0 && crow < min(cnt, c0 + rl);
+    const int lr = avalid ? crow - c0 : 0;
+    const uint8_t* arow_p = lds + (i < 8 ? L.a_hi : L.a_lo) + lr * L.RA + k0 + 16 * g;
+    const uint8_t* asc_p = lds + L.a_sc + lr * 2 * (a.H / 32) + (i < 8 ? 0 : a.H / 32) + b0;
+    uint4 p = *reinterpret_cast<const uint4*>(arow_p), q = *reinterpret_cast<const uint4*>(arow_p + 64);
+    uint32_t sw = *reinterpret_cast<const uint32_t*>(asc_p);
+    uint32_t gs = *reinterpret_cast<const uint32_t*>(lrow), us = *reinterpret_cast<const uint32_t*>(lrow + 32 * L.RS);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const uint4 p = zero_if(xa[s % PF], avalid), q = zero_if(xb[s % PF], avalid);
-      const int sa = avalid ? (int)byte_of(saw[s % PF], g) : 127;
-      if (s + PF < NS) { xa[s % PF] = xr[8 * (s + PF)]; xb[s % PF] = xr[8 * (s + PF) + 4]; saw[s % PF] = xs[s + PF]; }
-      v8i A = {(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, (int)q.z, (int)q.w};
-      accg = MFMA_F8xF4(A, b_operand(bg[s]), accg, sa, (int)byte_of(sgw[s], g));
-      accu = MFMA_F8xF4(A, b_operand(bu[s]), accu, sa, (int)byte_of(suw[s], g));
+      const uint4 pc = zero_if(p, avalid), qc = zero_if(q, avalid);
+      const int sa = avalid ? (int)byte_of(sw, g) : 127;
+      const int sgc = (int)byte_of(gs, g), suc = (int)byte_of(us, g);
+      if (s + 1 < NS) {
+        p = *reinterpret_cast<const uint4*>(arow_p + 128 * (s + 1));
+        q = *reinterpret_cast<const uint4*>(arow_p + 128 * (s + 1) + 64);
+        sw = *reinterpret_cast<const uint32_t*>(asc_p + 4 * (s + 1));
+        gs = *reinterpret_cast<const uint32_t*>(lrow + 4 * (s + 1));
+        us = *reinterpret_cast<const uint32_t*>(lrow + 32 * L.RS + 4 * (s + 1));
+      }
+      v8i A = {(int)pc.x, (int)pc.y, (int)pc.z, (int)pc.w, (int)qc.x, (int)qc.y, (int)qc.z, (int)qc.w};
+      accg = MFMA_F8xF4(A, b_operand(bg[s]), accg, sa, sgc);
+      accu = MFMA_F8xF4(A, b_operand(bu[s]), accu, sa, suc);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  run_pass(0);
+  for (int c0 = rl; c0 < cnt; c0 += rl) {   // rare: more rows routed to one expert than staged at once
+    __syncthreads();
+    stage_act_rows<JMAX>(a, lds, L, c0, min(cnt - c0, rl), tok, wave, lane);
+    wait_vm_all();
+    __syncthreads();
+    run_pass(c0);
   }
   float vg[4], vu[4];
 #pragma unroll
@@ -173,39 +277,44 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
     vg[q] = accg[q] + __shfl_xor(accg[q], 32, 64);
     vu[q] = accu[q] + __shfl_xor(accu[q], 32, 64);
   }
-  __shared__ float red[3][2][2][32][4];   // [K-range 1..3][ntile][gate/up][lane][q]
-  __shared__ float hl[8][32];
-  if (kr > 0 && lane < 32) {
+  __syncthreads();                 // the activation region is free: K-range partials and the h tile go there
+  float (*red)[2][2][32][4] = reinterpret_cast<float (*)[2][2][32][4]>(lds + L.red);   // [K-range][ntile][g/u][lane][q]
+  float (*hl)[32] = reinterpret_cast<float (*)[32]>(lds + L.hl);
+  if (lane < 32) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) { red[kr - 1][ntile][0][lane][q] = vg[q]; red[kr - 1][ntile][1][lane][q] = vu[q]; }
+    for (int q = 0; q < 4; ++q) { red[kr][ntile][0][lane][q] = vg[q]; red[kr][ntile][1][lane][q] = vu[q]; }
   }
   __syncthreads();
-  if (kr == 0 && lane < 32) {
-    const int n = n0 + i;
+  // SwiGLU, one (row, output) per thread: K-range partials summed in a fixed order (0, 1, 2, 3)
+  uint16_t hb = 0;
+  const int e_q = tid & 3, e_l = (tid >> 2) & 31, e_nt = (tid >> 7) & 1;
+  const int e_r = 4 * (e_l >> 4) + e_q, e_n = e_nt * 16 + (e_l & 15);
+  if (tid < 256) {
+    float gsum = red[0][e_nt][0][e_l][e_q], usum = red[0][e_nt][1][e_l][e_q];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = 4 * g + q;
-      float gsum = vg[q], usum = vu[q];
-#pragma unroll
-      for (int j = 0; j < 3; ++j) { gsum += red[j][ntile][0][lane][q]; usum += red[j][ntile][1][lane][q]; }
-      uint16_t gt = f32_to_bf16(gsum);
-      float gtf = bf16_to_f32(gt);
-      float ut = round_bf16(usum);
-      float sig = bf16_to_f32(a.sigtab[gt]);
-      float hv = round_bf16(round_bf16(gtf * sig) * ut);
-      if (r < cnt) a.h[((size_t)u * a.R + r) * a.I + n] = f32_to_bf16(hv);
-      else if (a.zero_pad && r < a.R) a.h[((size_t)u * a.R + r) * a.I + n] = 0;
-      hl[r][ntile * 16 + i] = r < cnt ? hv : 0.0f;
+    for (int j = 1; j < 4; ++j) {
+      const float pg = red[j][e_nt][0][e_l][e_q], pu = red[j][e_nt][1][e_l][e_q];
+      gsum += j < ksplit ? pg : 0.0f;
+      usum += j < ksplit ? pu : 0.0f;
     }
+    const uint16_t gt = f32_to_bf16(gsum);
+    const float gtf = bf16_to_f32(gt);
+    const float ut = round_bf16(usum);
+    const float sig = round_bf16(sigmoid_spec(gtf));   // the bf16 sigmoid table's entry for gt, computed in place
+    const float hv = round_bf16(round_bf16(gtf * sig) * ut);
+    hb = e_r < cnt ? f32_to_bf16(hv) : (uint16_t)0;
+    hl[e_r][e_n] = e_r < cnt ? hv : 0.0f;
   }
   __syncthreads();
+  if (a.zero_pad && tid < 256 && e_r < a.R)   // h itself only for callers that asked for the intermediates
+    a.h[((size_t)u * a.R + e_r) * a.I + nb + e_n] = hb;
   if (wave == 0) {                 // hi/lo E4M3 split of h per (row, 32-block): 8 lanes per row, 4 values each
     const int r = lane >> 3, nl = (lane & 7) * 4;
     float v[4];
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) { v[j] = hl[r][nl + j]; amax = fmaxf(amax, fabsf(v[j])); }
-    amax = group_max(amax, 8);
+    amax = dpp_group_max8(amax);
     const int X = fp8_block_exp(amax);
     uint32_t hw = 0, lw = 0;
     float res[4], ramax = 0.0f;
@@ -216,7 +325,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
       res[j] = v[j] - dec;
       ramax = fmaxf(ramax, fabsf(res[j]));
     }
-    ramax = group_max(ramax, 8);
+    ramax = dpp_group_max8(ramax);
     const int Y = fp8_block_exp(ramax);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -233,60 +342,147 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
       }
     }
   }
+  if (ROUTED) publish_routes(a, s_inds, s_w, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, tid);
 }
 
 // ------------------------------------------------------------------ Kernel B + combine (owner computes)
 // Block (1024 threads, 16 waves) owns 16 outputs m (blockIdx.x) for every distinct expert.  Work item
-// (u, K-half): wave w takes items w, w + 16, ...; per item its NS = I / 256 weight steps are loaded in one
-// batch, the activations a few steps ahead of their MFMA.  The two K-half dot products of each (expert,
-// row) land in LDS; the block adds them in a fixed order, applies the router weight (and the bf16 rounding
-// of the gather_qmm path when asked, model.py:181), sums each row's k routes in route order
+// (u, K-half): wave w takes items w, w + 16, ...  Per item, the wave first sends the expert's h rows for its
+// K-half straight to a wave-private LDS buffer (global_load_lds) and its weight scales to registers, then
+// issues its NS = I / 256 weight steps in one batch; a load issued after that batch would queue behind it.
+// The routing metadata and the combine inputs all come in with one round trip at the start.  The two K-half
+// dot products of each route land in LDS (one row per route: expert u's rows start at the sum of the
+// earlier experts' counts); the block adds them in a fixed order, applies the router weight (and the bf16
+// rounding of the gather_qmm path when asked, model.py:181), sums each row's k routes in route order
 // (kernels.py:198-199) and writes y.  No other block is waited for.
+
+// Per-wave LDS buffer of the down kernel for `rw` staged h rows of one K-half (KH = I / 2 codes):
+// hi rows (KH + 16 bytes each), lo rows (starting 128 bytes off the hi rows' bank phase), then per row the
+// [hi | lo] scales (2 x KH / 32 bytes).
+struct DownLds {
+  int KH, RA, hi, lo, sc, wave_bytes, part, total;
+};
+__host__ __device__ inline DownLds down_lds(int I, int rw, int nroutes) {
+  DownLds L;
+  L.KH = I / 2;
+  L.RA = L.KH + 16;
+  L.hi = 0;
+  L.lo = align_up(rw * L.RA, 256) + 128;
+  L.sc = align_up(L.lo + rw * L.RA, 16);
+  L.wave_bytes = align_up(L.sc + rw * 2 * (L.KH / 32), 256);
+  L.part = 16 * L.wave_bytes;                       // [2][nroutes][16] floats
+  L.total = L.part + 2 * nroutes * 16 * 4;
+  return L;
+}
+
 template <int NS>
-__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) decode_down_combine_kernel(ExpertsArgs a) {
-  extern __shared__ float plds[];     // [2][Umax * R][16] K-half dot products
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) decode_down_combine_kernel(ExpertsArgs a, int rw) {
+  extern __shared__ __align__(16) uint8_t dl[];
+  __shared__ uint32_t cgidx[64];      // combine indices and weights, loaded with the routing metadata
+  __shared__ float cuw[1024];
+  __shared__ int cpref[64], ccnt[64]; // first route row and row count of each distinct expert
+  constexpr int SRS = NS + 4;         // dwords per staged scale row (16-byte aligned, conflict-free row reads)
+  __shared__ __align__(16) uint32_t wsc[16][16 * SRS];   // per wave: the current item's 16 scale rows
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar registers)
   const int m0 = blockIdx.x * 16;
-  const int arow = i & 7;
   const int UR = a.Umax * a.R;
-  // the first item's metadata is loaded together with the expert count (one round trip)
-  int nxt_cnt = a.ucnt[min(wave >> 1, a.Umax - 1)], nxt_slot = a.uslot[min(wave >> 1, a.Umax - 1)];
+  const int nr = a.M * a.k;
+  const DownLds L = down_lds(a.I, rw, nr);
+  // one round trip: per-expert counts and slots (lane j holds expert j), the combine inputs, the count
+  const int ej = min(lane, a.Umax - 1);
+  const int cntv = min(max(a.ucnt[ej], 0), a.R), slotv = a.uslot[ej];
+  const uint32_t gi = a.gidx[min(tid, nr - 1)];
+  const float wi = a.uw[min(tid, UR - 1)];
   const int U = a.n_unique ? min(*a.n_unique, a.Umax) : a.Umax;
+  // first route row of expert j = sum of the earlier experts' counts (counts <= 8: four bit-plane ballots)
+  int prefv = 0;
+  {
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int c = lane < a.Umax ? cntv : 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) prefv += __popcll(__ballot((c >> b) & 1) & below) << b;
+  }
+  uint8_t* wb = dl + wave * L.wave_bytes;
+  // h rows of the item staged at rows 0 .. n - 1 (n <= 3) of the wave's buffer: hi and lo codes of the K-half
+  // (KH <= 1024 bytes, one piece each) and the [hi | lo] scales
+  auto stage = [&](int u, int kh, int c0, int n) {
+    const int sb = L.KH / 32;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      if (c >= n) break;
+      const size_t row = (size_t)u * a.R + c0 + c;
+      if (16 * lane < L.KH) {
+        lds_copy16(a.hq_hi + row * a.I + kh * L.KH, 16 * lane, wb + L.hi + c * L.RA);
+        lds_copy16(a.hq_lo + row * a.I + kh * L.KH, 16 * lane, wb + L.lo + c * L.RA);
+      }
+      const uint8_t* dst = wb + L.sc + c * 2 * sb;
+      if (4 * lane < sb) lds_copy4(a.hq_hs + row * (a.I / 32) + kh * sb, 4 * lane, dst);
+      else if (4 * lane < 2 * sb) lds_copy4(a.hq_ls + row * (a.I / 32) + kh * sb - sb, 4 * lane, dst);
+    }
+  };
+  // scale staging: lane L loads 8 bytes of row L / LPR of the item's K-half (NS * 4 bytes per row)
+  constexpr int LPR = NS / 2;
+  const int srow = min(lane / LPR, 15), spart = lane % LPR;
+  const int crow = i & 7;
+  float* part = reinterpret_cast<float*>(dl + L.part);
   for (int item = wave; item < 2 * U; item += 16) {
     const int u = item >> 1, kh = item & 1;
-    const int cnt = min(nxt_cnt, a.R);
-    const int slot = nxt_slot;
-    if (item + 16 < 2 * U) { nxt_cnt = a.ucnt[(item + 16) >> 1]; nxt_slot = a.uslot[(item + 16) >> 1]; }
+    const int cnt = __builtin_amdgcn_readlane(cntv, u);
+    const int slot = __builtin_amdgcn_readlane(slotv, u);
+    const int rbase = __builtin_amdgcn_readlane(prefv, u);
     const bool active = cnt > 0 && slot >= 0 && slot < a.S;
-    const bool avalid = active && arow < cnt;
-    const size_t hrow = (size_t)u * a.R + (avalid ? arow : 0);
+    if (active) stage(u, kh, 0, min(cnt, rw));
     const int b0 = kh * NS * 4;      // first 32-block of this K-half
-    const uint4* xr = reinterpret_cast<const uint4*>((i < 8 ? a.hq_hi : a.hq_lo) + hrow * a.I + b0 * 32) + g;
-    const uint32_t* xs = reinterpret_cast<const uint32_t*>((i < 8 ? a.hq_hs : a.hq_ls) + hrow * (a.I / 32) + b0);
-    const size_t brow = (size_t)(active ? slot : 0) * a.H + m0 + i;
-    const uint4* dw = reinterpret_cast<const uint4*>(a.down_w + brow * (a.I / 8)) + b0 + g;
-    const uint32_t* dsw = reinterpret_cast<const uint32_t*>(a.down_s + brow * (a.I / 32) + b0);
+    const size_t bslot = (size_t)(active ? slot : 0) * a.H + m0;
+    const uint4* dw = reinterpret_cast<const uint4*>(a.down_w + (bslot + i) * (a.I / 8)) + b0 + g;
+    const uint2 sraw = *(reinterpret_cast<const uint2*>(a.down_s + (bslot + srow) * (a.I / 32) + b0) + spart);
+    uint4 bw[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) bw[s] = dw[4 * s];
+    __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before anything waits
+    if (lane < 16 * LPR) *reinterpret_cast<uint2*>(&wsc[wave][srow * SRS + 2 * spart]) = sraw;
+    wait_vm_all();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    {
-      constexpr int PF = NS < 4 ? NS : 4;
-      uint4 bw[NS], xa[PF], xb[PF];
-      uint32_t sbw[NS], saw[PF];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) bw[s] = dw[4 * s];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) sbw[s] = dsw[s];
-#pragma unroll
-      for (int s = 0; s < PF; ++s) { xa[s] = xr[8 * s]; xb[s] = xr[8 * s + 4]; saw[s] = xs[s]; }
-      __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before the first MFMA
+    const uint32_t* srow_p = &wsc[wave][i * SRS];
+    // one pass over the staged rows: the operands of step s + 1 are read from LDS while step s multiplies
+    auto run_pass = [&](int c0) {
+      const bool avalid = crow >= c0 && crow < min(cnt, c0 + rw);
+      const int lr = avalid ? crow - c0 : 0;
+      const uint8_t* arow_p = wb + (i < 8 ? L.hi : L.lo) + lr * L.RA + 16 * g;
+      const uint8_t* asc_p = wb + L.sc + lr * 2 * (L.KH / 32) + (i < 8 ? 0 : L.KH / 32);
+      uint4 p = *reinterpret_cast<const uint4*>(arow_p), q = *reinterpret_cast<const uint4*>(arow_p + 64);
+      uint32_t sw = *reinterpret_cast<const uint32_t*>(asc_p), bs = srow_p[0];
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const uint4 p = zero_if(xa[s % PF], avalid), q = zero_if(xb[s % PF], avalid);
-        const int sa = avalid ? (int)byte_of(saw[s % PF], g) : 127;
-        if (s + PF < NS) { xa[s % PF] = xr[8 * (s + PF)]; xb[s % PF] = xr[8 * (s + PF) + 4]; saw[s % PF] = xs[s + PF]; }
-        v8i A = {(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, (int)q.z, (int)q.w};
-        acc = MFMA_F8xF4(A, b_operand(bw[s]), acc, sa, (int)byte_of(sbw[s], g));
+        const uint4 pc = zero_if(p, avalid), qc = zero_if(q, avalid);
+        const int sa = avalid ? (int)byte_of(sw, g) : 127;
+        const int sb = (int)byte_of(bs, g);
+        if (s + 1 < NS) {
+          p = *reinterpret_cast<const uint4*>(arow_p + 128 * (s + 1));
+          q = *reinterpret_cast<const uint4*>(arow_p + 128 * (s + 1) + 64);
+          sw = *reinterpret_cast<const uint32_t*>(asc_p + 4 * (s + 1));
+          bs = srow_p[s + 1];
+        }
+        v8i A = {(int)pc.x, (int)pc.y, (int)pc.z, (int)pc.w, (int)qc.x, (int)qc.y, (int)qc.z, (int)qc.w};
+        acc = MFMA_F8xF4(A, b_operand(bw[s]), acc, sa, sb);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    };
+    if (active) run_pass(0);
+    for (int c0 = rw; active && c0 < cnt; c0 += rw) {   // rare: more rows on one expert than the buffer holds
+      __builtin_amdgcn_wave_barrier();
+      stage(u, kh, c0, min(cnt - c0, rw));
+      wait_vm_all();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      run_pass(c0);
     }
+    __builtin_amdgcn_wave_barrier();     // the staged rows and scales are read before the next item overwrites them
     float dq[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) dq[q] = acc[q] + __shfl_xor(acc[q], 32, 64);   // hi rows + lo rows
@@ -294,17 +490,30 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = 4 * g + q;
-        if (r < a.R) plds[(kh * UR + u * a.R + r) * 16 + i] = (active && r < cnt) ? dq[q] : 0.0f;
+        if (r < cnt && rbase + r < nr) part[(kh * nr + rbase + r) * 16 + i] = dq[q];
       }
     }
   }
+  if (tid < nr) cgidx[tid] = gi;
+  if (tid < UR) cuw[tid] = wi;
+  if (tid < 64) { cpref[tid] = prefv; ccnt[tid] = lane < a.Umax ? cntv : 0; }
   __syncthreads();
+  // route row of a (u, c) index (u < U); -1 when it carries no route
+  auto route_row = [&](uint32_t idx) -> int {
+    const int u = (int)(idx / (uint32_t)a.R), c = (int)(idx % (uint32_t)a.R);
+    const int row = cpref[u] + c;
+    return (c < ccnt[u] && row < nr) ? row : -1;
+  };
   if (a.zero_pad) {          // copy of the partials (kernels.py:120) for callers that asked for them
     for (int e = tid; e < U * a.R * 16; e += blockDim.x) {
-      const int row = e >> 4, mi = e & 15;
-      float d = plds[row * 16 + mi] + plds[(UR + row) * 16 + mi];
+      const int ur = e >> 4, mi = e & 15;
+      const int u = ur / a.R, c = ur - u * a.R;
+      (void)u; (void)c;
+      float d = 0.0f;
+      const int row = route_row((uint32_t)ur);
+      if (row >= 0) d = part[row * 16 + mi] + part[(nr + row) * 16 + mi];
       if (a.round_bf16) d = round_bf16(d);
-      a.part[(size_t)row * a.H + m0 + mi] = d * a.uw[row];
+      a.part[(size_t)ur * a.H + m0 + mi] = d * cuw[ur];
     }
   }
   const uint32_t nrows = (uint32_t)(U * a.R);
@@ -312,11 +521,12 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const int row = e >> 4, mi = e & 15;
     float accy = 0.0f;
     for (int j = 0; j < a.k; ++j) {
-      const uint32_t idx = a.gidx[row * a.k + j];
-      if (idx < nrows) {
-        float d = plds[idx * 16 + mi] + plds[(UR + idx) * 16 + mi];
+      const uint32_t idx = cgidx[row * a.k + j];
+      const int pr = idx < nrows ? route_row(idx) : -1;
+      if (pr >= 0) {
+        float d = part[pr * 16 + mi] + part[(nr + pr) * 16 + mi];
         if (a.round_bf16) d = round_bf16(d);
-        accy = accy + d * a.uw[idx];
+        accy = accy + d * cuw[idx];
       }
     }
     a.y[(size_t)row * a.H + m0 + mi] = f32_to_bf16(accy);
@@ -355,50 +565,86 @@ static int check_bank(const mimo_bank* b) {
                MIMO_ERR_SHAPE, "bank: need hidden in {256, 512, 1024, 2048, 4096} and inter in {512, 1024, 2048} (got "
                "H=%d I=%d)", b->hidden, b->inter);
   MIMO_REQUIRE(((reinterpret_cast<uintptr_t>(b->gate_s) | reinterpret_cast<uintptr_t>(b->up_s) |
-                 reinterpret_cast<uintptr_t>(b->down_s)) & 3) == 0,
-               MIMO_ERR_ALIGN, "bank: scale pools must be 4-byte aligned");
+                 reinterpret_cast<uintptr_t>(b->down_s)) & 7) == 0,
+               MIMO_ERR_ALIGN, "bank: scale pools must be 8-byte aligned");
   MIMO_REQUIRE(aligned16(b->gate_w) && aligned16(b->up_w) && aligned16(b->down_w), MIMO_ERR_ALIGN,
                "bank: weight pools must be 16-byte aligned");
+  return MIMO_OK;
+}
+
+// Dynamic LDS above the default 64 KB has to be allowed per kernel once.
+static int allow_lds(const void* fn, size_t bytes, int* allowed) {
+  if ((int)bytes <= 65536 || (int)bytes <= *allowed) return MIMO_OK;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess)
+    return set_error(MIMO_ERR_HIP, "hipFuncSetAttribute(%zu bytes of LDS): %s", bytes, hipGetErrorString(e));
+  *allowed = (int)bytes;
+  return MIMO_OK;
+}
+
+template <int NS, bool ROUTED>
+static int launch_gateup(const ExpertsArgs& a, int rl, hipStream_t st) {
+  static int allowed = 0;
+  const size_t lds = (size_t)gateup_lds(a.H, rl).total;
+  int rc = allow_lds(reinterpret_cast<const void*>(&decode_gateup_kernel<NS, ROUTED>), lds, &allowed);
+  if (rc) return rc;
+  decode_gateup_kernel<NS, ROUTED><<<dim3(a.I / 32, a.Umax), 512, lds, st>>>(a, rl);
+  return MIMO_OK;
+}
+
+template <int NS>
+static int launch_down(const ExpertsArgs& a, int rw, hipStream_t st) {
+  static int allowed = 0;
+  const size_t lds = (size_t)down_lds(a.I, rw, a.M * a.k).total;
+  int rc = allow_lds(reinterpret_cast<const void*>(&decode_down_combine_kernel<NS>), lds, &allowed);
+  if (rc) return rc;
+  decode_down_combine_kernel<NS><<<a.H / 16, 1024, lds, st>>>(a, rw);
   return MIMO_OK;
 }
 
 static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream_t st) {
   ExpertsArgs a = base;
   a.round_bf16 = round_bf16;
-  dim3 g1(a.I / 32, a.Umax);
   const int ns = gateup_steps(a.H);    // MFMA steps per wave
-  if (a.scores && a.Umax > 16) {
+  // activation rows staged at once: a row picks an expert at most once, so an expert gets at most M rows;
+  // more (a slot table mapping two experts of a row to one slot) costs extra passes, not wrong results
+  const bool fused_select = a.scores && a.Umax <= 16 && a.E <= 256;   // small batches: every block selects
+  const int rl = min(a.R, fused_select ? min(M, 2) : M);   // the routed kernel stages at most 2 rows at once
+  const int rw = min(min(a.R, M), 3);
+  if (a.scores && !fused_select) {
     int rc = launch_select_group(a.scores, a.keys, a.M, a.E, a.k, a.slot_of, a.R, a.S, a.Umax, a.inds_out, a.w_out,
                                  a.rt_uids, a.rt_urows, a.rt_ucnt, a.rt_uw, a.rt_gidx, a.rt_nu, a.rt_status, st);
     if (rc) return rc;
   }
+  int rc;
   {
     ProfScope p(st, "decode_gateup");
-    if (a.scores && a.Umax <= 16) {   // small batches: every block selects (cheaper than a launch)
+    if (fused_select) {   // cheaper than a separate selection launch
       switch (ns) {
-        case 8: decode_gateup_kernel<8, true><<<g1, 512, 0, st>>>(a); break;
-        case 4: decode_gateup_kernel<4, true><<<g1, 512, 0, st>>>(a); break;
-        case 2: decode_gateup_kernel<2, true><<<g1, 512, 0, st>>>(a); break;
-        default: decode_gateup_kernel<1, true><<<g1, 512, 0, st>>>(a); break;
+        case 8: rc = launch_gateup<8, true>(a, rl, st); break;
+        case 4: rc = launch_gateup<4, true>(a, rl, st); break;
+        case 2: rc = launch_gateup<2, true>(a, rl, st); break;
+        default: rc = launch_gateup<1, true>(a, rl, st); break;
       }
     } else {
       switch (ns) {
-        case 8: decode_gateup_kernel<8, false><<<g1, 512, 0, st>>>(a); break;
-        case 4: decode_gateup_kernel<4, false><<<g1, 512, 0, st>>>(a); break;
-        case 2: decode_gateup_kernel<2, false><<<g1, 512, 0, st>>>(a); break;
-        default: decode_gateup_kernel<1, false><<<g1, 512, 0, st>>>(a); break;
+        case 8: rc = launch_gateup<8, false>(a, rl, st); break;
+        case 4: rc = launch_gateup<4, false>(a, rl, st); break;
+        case 2: rc = launch_gateup<2, false>(a, rl, st); break;
+        default: rc = launch_gateup<1, false>(a, rl, st); break;
       }
     }
   }
-  const size_t lds = 2 * (size_t)a.Umax * a.R * 16 * sizeof(float);
+  if (rc) return rc;
   {
     ProfScope p(st, "decode_down_combine");
     switch (a.I / 256) {
-      case 8: decode_down_combine_kernel<8><<<a.H / 16, 1024, lds, st>>>(a); break;
-      case 4: decode_down_combine_kernel<4><<<a.H / 16, 1024, lds, st>>>(a); break;
-      default: decode_down_combine_kernel<2><<<a.H / 16, 1024, lds, st>>>(a); break;
+      case 8: rc = launch_down<8>(a, rw, st); break;
+      case 4: rc = launch_down<4>(a, rw, st); break;
+      default: rc = launch_down<2>(a, rw, st); break;
     }
   }
+  if (rc) return rc;
   return check_launch("moe experts");
 }
 
@@ -421,17 +667,16 @@ int mimo_moe_experts(const uint16_t* x, int M, const mimo_bank* bank, const int3
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && uslot && urows && ucnt && uw && gidx && y, MIMO_ERR_ARG, "moe_experts: null pointer");
-  MIMO_REQUIRE(M >= 1 && M <= 8 && R >= 1 && R <= 8 && k >= 1 && Umax >= 1 && Umax <= M * k && Umax * R <= 1024,
-               MIMO_ERR_SHAPE, "moe_experts: need 1 <= M <= 8, 1 <= R <= 8, 1 <= Umax <= M*k, Umax*R <= 1024");
+  MIMO_REQUIRE(M >= 1 && M <= 8 && R >= 1 && R <= 8 && k >= 1 && M * k <= 64 && Umax >= 1 && Umax <= M * k &&
+                   Umax * R <= 1024,
+               MIMO_ERR_SHAPE, "moe_experts: need 1 <= M <= 8, 1 <= R <= 8, M*k <= 64, 1 <= Umax <= M*k, "
+               "Umax*R <= 1024");
   MIMO_REQUIRE(aligned16(x) && aligned16(y) && (!part_out || aligned16(part_out)), MIMO_ERR_ALIGN,
                "moe_experts: x, y, part_out must be 16-byte aligned");
   const int H = bank->hidden, I = bank->inter;
   Carve c(ws, ws_bytes);
   ExpertsWs w = carve_experts(c, M, Umax, R, H, I);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_experts: workspace too small (need %zu)", c.off);
-  int err;
-  const uint16_t* sig = sigtab_device(&err);
-  if (!sig) return err;
   hipStream_t st = as_stream(stream);
   rc = launch_quantize_fp8_hilo(x, M, H, w.xq_hi, w.xq_hs, w.xq_lo, w.xq_ls, st);
   if (rc) return rc;
@@ -441,7 +686,6 @@ int mimo_moe_experts(const uint16_t* x, int M, const mimo_bank* bank, const int3
   a.gate_s = bank->gate_s; a.up_s = bank->up_s; a.down_s = bank->down_s;
   a.H = H; a.I = I; a.R = R; a.Umax = Umax; a.k = k; a.M = M; a.S = bank->n_slots;
   a.uslot = uslot; a.urows = urows; a.ucnt = ucnt; a.n_unique = n_unique; a.uw = uw; a.gidx = gidx;
-  a.sigtab = sig;
   a.h = h_out ? h_out : w.h;
   a.hq_hi = w.hq_hi; a.hq_lo = w.hq_lo; a.hq_hs = w.hq_hs; a.hq_ls = w.hq_ls;
   a.part = part_out ? part_out : w.part;
@@ -500,9 +744,6 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
                &gidx, &nu, &status);
   ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_decode: workspace too small (need %zu)", c.off);
-  int err;
-  const uint16_t* sig = sigtab_device(&err);
-  if (!sig) return err;
   hipStream_t st = as_stream(stream);
 
   RouterSmallArgs ra{};
@@ -518,7 +759,6 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
   a.gate_s = bank->gate_s; a.up_s = bank->up_s; a.down_s = bank->down_s;
   a.H = H; a.I = I; a.R = kDecodeR; a.Umax = Umax; a.k = k; a.M = M; a.S = S;
   a.uslot = uids; a.urows = urows; a.ucnt = ucnt; a.n_unique = nu; a.uw = uw; a.gidx = gidx;
-  a.sigtab = sig;
   a.h = ew.h; a.hq_hi = ew.hq_hi; a.hq_lo = ew.hq_lo; a.hq_hs = ew.hq_hs; a.hq_ls = ew.hq_ls;
   a.part = ew.part; a.zero_pad = 0; a.y = y;
   a.scores = scores; a.keys = keys; a.E = E; a.slot_of = slot_of;

@@ -13,10 +13,10 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 
 // round-to-nearest-even float -> bf16 bits; NaN stays a quiet NaN
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t n = (u >> 16) | 0x40u;
+  return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? n : r);
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
@@ -39,17 +39,19 @@ __device__ __forceinline__ uint32_t e2m1_mag_code(float y) {
 // ------------------------------------------------------------------ E4M3 (activation hi/lo split)
 // magnitude code for 0 <= y <= 448 (y exactly representable scaling of a bf16 value), nearest-even.
 __device__ __forceinline__ uint32_t e4m3_mag_code(float y) {
-  if (y < 0.015625f) {                       // below 2^-6: subnormal, quantum 2^-9
-    return (uint32_t)rintf(y * 512.0f);      // 8 == smallest normal, same encoding
-  }
-  uint32_t u = __float_as_uint(y);
+  // below 2^-6: subnormal, quantum 2^-9 (a result of 8 is the smallest normal, same encoding)
+  const uint32_t sub = (uint32_t)rintf(y * 512.0f);
+  const uint32_t u = __float_as_uint(y);
   int e = (int)((u >> 23) & 0xFF) - 127;
-  uint32_t f = u & 0x7FFFFFu;
-  uint32_t q = f >> 20, rem = f & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ++q;
-  if (q == 8u) { q = 0; ++e; }
+  const uint32_t f = u & 0x7FFFFFu;
+  uint32_t q = f >> 20;
+  const uint32_t rem = f & 0xFFFFFu;
+  q += (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ? 1u : 0u;
+  e += q == 8u ? 1 : 0;
+  q = q == 8u ? 0u : q;
   uint32_t code = ((uint32_t)(e + 7) << 3) | q;
-  return code > 0x7Eu ? 0x7Eu : code;
+  code = code > 0x7Eu ? 0x7Eu : code;
+  return y < 0.015625f ? sub : code;
 }
 __device__ __forceinline__ float e4m3_decode_mag(uint32_t c) {
   uint32_t e = (c >> 3) & 0xF, m = c & 7;
@@ -106,14 +108,17 @@ __device__ __forceinline__ double exp_spec(double x) {
   return __builtin_ldexp(p, (int)n);
 }
 // fp32 sigmoid = fp32(1 / (1 + exp_spec(-x))), input clamped to [-200, 200]; NaN -> canonical quiet NaN.
+// Branch-free, so that independent evaluations interleave.
 __device__ __forceinline__ float sigmoid_spec(float xf) {
 #pragma clang fp contract(off)
-  if (xf != xf) return __uint_as_float(0x7FC00000u);
-  double x = (double)xf;
-  if (x < -200.0) x = -200.0;
-  if (x > 200.0) x = 200.0;
-  double e = exp_spec(-x);
-  return (float)(1.0 / (1.0 + e));
+  const bool nan = xf != xf;
+  double x = nan ? 0.0 : (double)xf;
+  x = x < -200.0 ? -200.0 : x;
+  x = x > 200.0 ? 200.0 : x;
+  const double e = exp_spec(-x);
+  float s = (float)(1.0 / (1.0 + e));
+  asm volatile("" : "+v"(s));   // evaluated for every lane: keeps the compiler from branching around it
+  return nan ? __uint_as_float(0x7FC00000u) : s;
 }
 
 // 32 bf16-valued floats -> hi / lo E4M3 words (4 codes per word, element order) and E8M0 bytes:
@@ -179,6 +184,14 @@ __device__ __forceinline__ float group_max(float v, int width) {
   return v;
 }
 
+// max over each group of 8 consecutive lanes through DPP (xor 1, xor 2 within quads, then the half-row mirror)
+__device__ __forceinline__ float dpp_group_max8(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  return v;
+}
+
 // wave64 max / min of a uint32 through DPP row operations (xor 1, xor 2, half-row and row mirrors, then the
 // row_bcast15 / row_bcast31 steps across rows); every lane receives the result read from lane 63.
 __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
@@ -202,11 +215,44 @@ __device__ __forceinline__ uint32_t dpp_min_u32(uint32_t v) {
 
 // order-preserving map of an fp32 key to uint32 (NaN lowest, -0 treated as +0)
 __device__ __forceinline__ uint32_t key_to_ordered(float k) {
-  if (k != k) return 0u;
-  if (k == 0.0f) k = 0.0f;
-  uint32_t u = __float_as_uint(k);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  const uint32_t u = __float_as_uint(k == 0.0f ? 0.0f : k);
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return k != k ? 0u : o;
 }
+
+// ------------------------------------------------------------------ global -> LDS copies
+// global_load_lds: lane l's 16 (or 4) bytes at gbase + voff land at lds_dst + 16 l (or 4 l), without passing
+// through registers.  gbase and lds_dst must be wave-uniform (they go to SGPRs and M0).  Issued from inline
+// assembly so that the compiler's wait-counter bookkeeping does not pin the address registers (it would wait
+// for every outstanding load before reusing them); the caller waits with wait_vm_all() before any wave reads
+// the data.  M0 is only a launch-time scratch register on gfx950 (ordinary LDS instructions do not use it).
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"     // M0 is declared clobbered on purpose
+__device__ __forceinline__ void lds_copy16(const void* gbase, uint32_t voff, const void* lds_dst) {
+  const uint64_t b = uniform_u64((uint64_t)gbase);
+  const uint32_t m = lds_addr(lds_dst);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(m)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* gbase, uint32_t voff, const void* lds_dst) {
+  const uint64_t b = uniform_u64((uint64_t)gbase);
+  const uint32_t m = lds_addr(lds_dst);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(b), "s"(m)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every global load of the wave has landed,
+// including the global -> LDS copies above
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // ------------------------------------------------------------------ misc
 __device__ __forceinline__ uint32_t load_u8x4(const uint8_t* p) { return *(const uint32_t*)p; }

@@ -148,12 +148,11 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
 // One block, one wave per row: top-k and renormalisation, then wave 0 groups the routes by slot.
 __global__ void __launch_bounds__(512) router_select_group_kernel(SelectGroupArgs a) {
   const int wave = threadIdx.x >> 6;
-  __shared__ int sel[8][32];
+  __shared__ int sel[8][kSelLds];
   __shared__ int32_t s_inds[64];
   __shared__ float s_w[64];
   __shared__ int lurows[512];
   __shared__ float luw[512];
-  __shared__ uint32_t bits[32];
   if (wave < a.T)
     wave_select_row(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k, s_w + wave * a.k,
                     sel[wave]);
@@ -164,7 +163,7 @@ __global__ void __launch_bounds__(512) router_select_group_kernel(SelectGroupArg
   }
   if (wave == 0)
     wave_group_routes(s_inds, s_w, a.slot_of, a.T, a.k, a.R, a.n_slots, a.Umax, a.uids, a.urows, a.ucnt, a.uw,
-                      a.gidx, a.n_unique, a.status, lurows, luw, bits);
+                      a.gidx, a.n_unique, a.status, lurows, luw);
 }
 
 int launch_select_group(const float* scores, const float* keys, int T, int E, int k, const int32_t* slot_of, int R,
@@ -231,7 +230,7 @@ __global__ void __launch_bounds__(256) router_select_kernel(const float* __restr
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float* s_row = sm + wave * 2 * E;
   float* k_row = s_row + E;
-  __shared__ int sel[4][32];
+  __shared__ int sel[4][kSelLds];
   __shared__ int32_t oi[4][16];
   __shared__ float ow[4][16];
   const int t = blockIdx.x * 4 + wave;
@@ -261,11 +260,10 @@ __global__ void group_routes_kernel(const int32_t* inds, const float* scores, co
                                     float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status) {
   __shared__ int present[1024];
   __shared__ int route_slot[1024];
-  __shared__ uint32_t bits[32];
   if (M * k <= 64 && Umax * R <= 1024) {
     if (threadIdx.x < 64)
       wave_group_routes(inds, scores, slot_of, M, k, R, n_slots, Umax, uids, urows, ucnt, uw, gidx, n_unique, status,
-                        present, reinterpret_cast<float*>(route_slot), bits);
+                        present, reinterpret_cast<float*>(route_slot));
     return;
   }
   block_group_routes(inds, scores, slot_of, M, k, R, n_slots, Umax, uids, urows, ucnt, uw, gidx, n_unique, status,

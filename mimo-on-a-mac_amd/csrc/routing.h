@@ -10,49 +10,78 @@
 namespace mimo {
 
 // ------------------------------------------------------------------ selection (one wave per row)
-// Lane l owns candidates e = l + 64 j (j < PER).  It sorts them once (descending key; ids increase with j, so
-// the sort keeps the lower id first on equal keys); then each of the k rounds takes the maximum head key over
-// the wave (DPP), the minimum id among lanes whose head carries it, and the winning lane shifts its list.
-// Keys are fp32 mapped to an order-preserving uint32 plus one (0 = exhausted; NaN sorts lowest).
+// Lane l owns candidates e = l + 64 j (j < PER), keyed by the fp32 key mapped to an order-preserving uint32
+// plus one (0 = no candidate; NaN keys map to 1 and sort lowest).  A bisection on that key finds the k-th
+// largest value T (count(key >= T) >= k > count(key > T)), each step one ballot per candidate slot and
+// scalar popcounts, stopping early once exactly k keys reach the midpoint.  The selection is every key above
+// T plus the lowest-id keys equal to T; its k entries are then ranked by (key descending, id ascending) in
+// LDS.  Renormalisation sums the scores sequentially in that order.
+constexpr int kSelLds = 80;   // ints of LDS scratch per selecting wave (k <= 16)
 template <int PER>
-__device__ inline void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
-                                         int32_t* inds_out, float* w_out, int* lds_sel) {
+__device__ __forceinline__ void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
+                                                  int32_t* inds_out, float* w_out, int* lds_sel) {
   const int lane = threadIdx.x & 63;
-  float* lds_s = reinterpret_cast<float*>(lds_sel + 16);   // lds_sel has room for 32 entries
-  uint32_t cv[PER], id[PER];
-  float sc[PER];
+  uint32_t* t_key = reinterpret_cast<uint32_t*>(lds_sel);        // [16] selected, in (j, lane) order
+  int* t_id = lds_sel + 16;
+  float* t_sc = reinterpret_cast<float*>(lds_sel + 32);
+  int* f_id = lds_sel + 48;                                        // [16] in canonical order
+  float* f_sc = reinterpret_cast<float*>(lds_sel + 64);
+  uint32_t cv[PER];
+  float sc[PER], kv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {            // every load in flight before any is used
+    const int e = lane + 64 * j;
+    kv[j] = key_row[e < E ? e : 0];
+    sc[j] = s_row[e < E ? e : 0];
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) cv[j] = (lane + 64 * j) < E ? key_to_ordered(kv[j]) + 1u : 0u;
+  // count(cv >= lo) >= k (every candidate has cv >= 1 and E >= k); count(cv >= hi) < k (cv < 2^32 - 1)
+  uint32_t lo = 1u, hi = 0xFFFFFFFFu;
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) c += __popcll(__ballot(cv[j] >= mid));
+    if (c >= k) lo = mid; else hi = mid;
+    if (c == k) break;
+  }
+  const uint32_t T = lo;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int ngt = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) ngt += __popcll(__ballot(cv[j] > T));
+  const int need = k - ngt;                  // keys equal to T that are taken, lowest ids first
+  int ties_before = 0, sel_before = 0;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int e = lane + 64 * j;
-    const bool ok = e < E;
-    const float kv = key_row[ok ? e : 0];
-    sc[j] = s_row[ok ? e : 0];
-    cv[j] = ok ? key_to_ordered(kv) + 1u : 0u;
-    id[j] = (uint32_t)e;
-  }
-  // odd-even transposition sort, descending by value, stable on equal values
-#pragma unroll
-  for (int pass = 0; pass < PER; ++pass) {
-#pragma unroll
-    for (int j = pass & 1; j + 1 < PER; j += 2) {
-      if (cv[j + 1] > cv[j]) {
-        uint32_t t = cv[j]; cv[j] = cv[j + 1]; cv[j + 1] = t;
-        t = id[j]; id[j] = id[j + 1]; id[j + 1] = t;
-        float f = sc[j]; sc[j] = sc[j + 1]; sc[j + 1] = f;
-      }
+    const uint64_t tie = __ballot(cv[j] == T);
+    const bool take = cv[j] > T || (cv[j] == T && ties_before + __popcll(tie & below) < need);
+    const uint64_t sel = __ballot(take);
+    if (take) {
+      const int pos = sel_before + __popcll(sel & below);
+      t_key[pos] = cv[j];
+      t_id[pos] = lane + 64 * j;
+      t_sc[pos] = sc[j];
     }
+    ties_before += __popcll(tie);
+    sel_before += __popcll(sel);
   }
-  for (int r = 0; r < k; ++r) {
-    const uint32_t kmax = dpp_max_u32(cv[0]);
-    const uint32_t myid = (cv[0] == kmax) ? id[0] : 0xFFFFFFFFu;
-    const uint32_t idmin = dpp_min_u32(myid);   // ties between lanes go to the lower expert id
-    if (myid == idmin) {
-      lds_sel[r] = (int)idmin;
-      lds_s[r] = sc[0];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (lane < k) {
+    const uint32_t mk = t_key[lane];
+    const int mi = t_id[lane];
+    int rank = 0;
 #pragma unroll
-      for (int j = 0; j + 1 < PER; ++j) { cv[j] = cv[j + 1]; id[j] = id[j + 1]; sc[j] = sc[j + 1]; }
-      cv[PER - 1] = 0u;
+    for (int t = 0; t < 16; ++t) {            // k <= 16; reads batched, entries past k ignored
+      const uint32_t ok = t_key[t];
+      const int oi = t_id[t];
+      rank += (t < k && (ok > mk || (ok == mk && oi < mi))) ? 1 : 0;
     }
+    f_id[rank] = mi;
+    f_sc[rank] = t_sc[lane];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
@@ -61,22 +90,26 @@ __device__ inline void wave_select_row_t(const float* s_row, const float* key_ro
   float denom = 0.0f;
   if (lane == 0) {
 #pragma clang fp contract(off)
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = f_sc[r];
     float acc = 0.0f;
-    for (int r = 0; r < k; ++r) acc = acc + lds_s[r];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc = r < k ? acc + v[r] : acc;
     denom = acc + 1e-20f;
   }
   denom = __shfl(denom, 0, 64);
   if (lane < k) {
 #pragma clang fp contract(off)
-    float wv = lds_s[lane] / denom;
+    float wv = f_sc[lane] / denom;
     if (scaling != 1.0f) wv = wv * scaling;
-    inds_out[lane] = lds_sel[lane];
+    inds_out[lane] = f_id[lane];
     w_out[lane] = wv;
   }
   __builtin_amdgcn_wave_barrier();
 }
 
-__device__ inline void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,
+__device__ __forceinline__ void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,
                                        int32_t* inds_out, float* w_out, int* lds_sel) {
   if (E <= 64) wave_select_row_t<1>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
   else if (E <= 128) wave_select_row_t<2>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
@@ -86,12 +119,14 @@ __device__ inline void wave_select_row(const float* s_row, const float* key_row,
 }
 
 // ------------------------------------------------------------------ grouping (one wave, <= 64 routes)
-// The same outputs as block_group_routes from shuffles only: route t on lane t; lower = earlier routes of its
-// slot (= its row slot c), rank = distinct smaller slots (= u).  lurows/luw: LDS scratch of Umax*R entries.
-__device__ inline void wave_group_routes(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k,
-                                  int R, int n_slots, int Umax, int32_t* uids, int32_t* urows, int32_t* ucnt,
-                                  float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status, int* lurows,
-                                  float* luw, uint32_t* bits) {
+// The same outputs as block_group_routes from ballots only: route t on lane t.  One pass over the slot bits,
+// high to low, keeps `match` = live lanes that agree with this lane's slot on the bits seen so far; a lane
+// dropped at a bit where this lane has a 1 holds a smaller slot.  lower = earlier routes of the slot (= the
+// route's row position c), rank = distinct smaller slots (= u).  lurows/luw: LDS scratch of Umax*R entries.
+__device__ __forceinline__ void wave_group_routes(const int32_t* inds, const float* scores, const int32_t* slot_of,
+                                                  int M, int k, int R, int n_slots, int Umax, int32_t* uids,
+                                                  int32_t* urows, int32_t* ucnt, float* uw, uint32_t* gidx,
+                                                  int32_t* n_unique, int32_t* status, int* lurows, float* luw) {
   const int lane = threadIdx.x & 63;
   const int nr = M * k;
   int bad = 0;
@@ -103,35 +138,22 @@ __device__ inline void wave_group_routes(const int32_t* inds, const float* score
     if (s < 0 || s >= n_slots) { bad = MIMO_ERR_SLOT; s = 0; }
     sc = scores[lane];
   }
-  // lanes holding the same slot: AND of per-bit ballots (slot ids < 1024)
   const uint64_t live = __ballot(lane < nr);
-  uint64_t match = live;
-#pragma unroll
-  for (int b = 0; b < 10; ++b) {
-    const uint64_t m = __ballot((s >> b) & 1);
-    match &= ((s >> b) & 1) ? m : ~m;
+  const int nbits = n_slots > 1 ? 32 - __clz(n_slots - 1) : 1;      // slot ids are < n_slots
+  uint64_t match = live, smaller = 0ull;
+  for (int b = nbits - 1; b >= 0; --b) {
+    const bool one = (s >> b) & 1;
+    const uint64_t m = __ballot(one);
+    smaller |= one ? (match & ~m) : 0ull;
+    match &= one ? m : ~m;
   }
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int lower = __popcll(match & below);       // earlier routes of this slot = the route's row slot c
   const int same = __popcll(match);
-  const int first = (lane < nr && lower == 0) ? 1 : 0;
-  const int U = __popcll(__ballot(first));
-  // rank of the slot among the distinct slots (= u): bitmap of present slots in LDS
-  if (lane < 32) bits[lane] = 0u;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  if (first) atomicOr(&bits[s >> 5], 1u << (s & 31));
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  int rank = 0;
-  const int sw = s >> 5;
-#pragma unroll
-  for (int w = 0; w < 32; ++w) {
-    const uint32_t bw = bits[w];
-    rank += w < sw ? __popc(bw) : (w == sw ? __popc(bw & ((1u << (s & 31)) - 1u)) : 0);
-  }
+  const bool first = lane < nr && lower == 0;
+  const uint64_t firsts = __ballot(first);
+  const int U = __popcll(firsts);
+  const int rank = __popcll(smaller & firsts);     // distinct slots below this one
   for (int e = lane; e < Umax * R; e += 64) { lurows[e] = 0; luw[e] = 0.0f; }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
