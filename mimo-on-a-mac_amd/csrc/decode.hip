@@ -133,6 +133,21 @@ __device__ __forceinline__ void stage_act_rows(const ExpertsArgs& a, uint8_t* ld
   }
 }
 
+// Routes of one decode step for a block: wave r selects row r (top-k and renormalisation), wave 0 groups the
+// routes by slot (E <= 256).
+__device__ __forceinline__ void full_routing(const ExpertsArgs& a, int (*sel)[kSelLds], int32_t* s_inds, float* s_w,
+                                             int* lurows, float* luw, int32_t* g_uids, int32_t* g_urows,
+                                             int32_t* g_ucnt, float* g_uw, uint32_t* g_gidx, int32_t* g_nu, int wave) {
+  if (wave < a.M)
+    wave_select_row_t<4>(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k,
+                         s_w + wave * a.k, sel[wave]);
+  __syncthreads();
+  if (wave == 0)
+    wave_group_routes(s_inds, s_w, a.slot_of, a.M, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
+                      &g_nu[0], &g_nu[1], lurows, luw);
+  __syncthreads();
+}
+
 // Block (0, 0) of the routed gate/up kernel writes the step's routes and grouping for the down kernel (and the
 // caller's inds/w), after its own loads: stores ahead of the weight loads would make them wait.
 __device__ __forceinline__ void publish_routes(const ExpertsArgs& a, const int32_t* s_inds, const float* s_w,
@@ -166,17 +181,33 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar registers)
   int U, cnt_raw, slot, tok;          // tok: lane c < R holds the token of the expert's row c
-  if (ROUTED) {
+  // one row with expert ids as slots: a block needs only its expert, the u-th selected one in ascending id order
+  const bool fast = ROUTED && a.M == 1 && a.slot_of == nullptr && a.S >= a.E;
+  __shared__ int fast_slot[16];
+  if (ROUTED && fast) {
+    if (wave == 0) {
+      uint32_t cv[4];
+      bool take[4];
+      wave_load_keys<4>(a.keys, a.E, cv);              // E <= 256 on this path
+      wave_select_set<4>(cv, a.k, take);
+      const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      int before = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t sel = __ballot(take[j]);
+        if (take[j]) fast_slot[before + __popcll(sel & below)] = lane + 64 * j;
+        before += __popcll(sel);
+      }
+    }
+    __syncthreads();
+    U = a.k;                                            // distinct experts, one row each
+    cnt_raw = 1;
+    slot = u < U ? fast_slot[u] : 0;
+    tok = 0;
+  } else if (ROUTED) {
     // routes of this step: wave r selects row r (top-k and renormalisation), wave 0 groups them by slot; every
     // block does this (it costs less than a separate launch) and block (0, 0) publishes the result at its end
-    if (wave < a.M)
-      wave_select_row_t<4>(a.scores + wave * a.E, a.keys + wave * a.E, a.E, a.k, 1.0f, s_inds + wave * a.k,
-                           s_w + wave * a.k, sel[wave]);     // E <= 256 on this path
-    __syncthreads();
-    if (wave == 0)
-      wave_group_routes(s_inds, s_w, a.slot_of, a.M, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
-                        &g_nu[0], &g_nu[1], lurows, luw);
-    __syncthreads();
+    full_routing(a, sel, s_inds, s_w, lurows, luw, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, wave);
     U = g_nu[0];
     cnt_raw = g_ucnt[u];
     slot = g_uids[u];
@@ -308,41 +339,37 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   __syncthreads();
   if (a.zero_pad && tid < 256 && e_r < a.R)   // h itself only for callers that asked for the intermediates
     a.h[((size_t)u * a.R + e_r) * a.I + nb + e_n] = hb;
-  if (wave == 0) {                 // hi/lo E4M3 split of h per (row, 32-block): 8 lanes per row, 4 values each
-    const int r = lane >> 3, nl = (lane & 7) * 4;
-    float v[4];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { v[j] = hl[r][nl + j]; amax = fmaxf(amax, fabsf(v[j])); }
-    amax = dpp_group_max8(amax);
+  if (tid < 256) {                 // hi/lo E4M3 split of h per (row, 32-block): one value per lane, a row per half-wave
+    const int r = tid >> 5, nl = tid & 31;
+    const float v = hl[r][nl];
+    // max over the 32 lanes of the row: DPP within each 16-lane row, then one exchange between the two rows
+    float amax = dpp_group_max16(fabsf(v));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     const int X = fp8_block_exp(amax);
-    uint32_t hw = 0, lw = 0;
-    float res[4], ramax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float dec;
-      hw |= e4m3_encode(v[j], X, &dec) << (8 * j);
-      res[j] = v[j] - dec;
-      ramax = fmaxf(ramax, fabsf(res[j]));
-    }
-    ramax = dpp_group_max8(ramax);
+    float dec;
+    const uint32_t hc = e4m3_encode(v, X, &dec);
+    const float res = v - dec;
+    float ramax = dpp_group_max16(fabsf(res));
+    ramax = fmaxf(ramax, __shfl_xor(ramax, 16, 64));
     const int Y = fp8_block_exp(ramax);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float dec;
-      lw |= e4m3_encode(res[j], Y, &dec) << (8 * j);
-    }
+    const uint32_t lc = e4m3_encode(res, Y, &dec);
     if (r < cnt) {
       const size_t row = (size_t)u * a.R + r;
-      *reinterpret_cast<uint32_t*>(a.hq_hi + row * a.I + nb + nl) = hw;
-      *reinterpret_cast<uint32_t*>(a.hq_lo + row * a.I + nb + nl) = lw;
-      if ((lane & 7) == 0) {
+      a.hq_hi[row * a.I + nb + nl] = (uint8_t)hc;
+      a.hq_lo[row * a.I + nb + nl] = (uint8_t)lc;
+      if (nl == 0) {
         a.hq_hs[row * (a.I / 32) + blockIdx.x] = (uint8_t)(X + 127);
         a.hq_ls[row * (a.I / 32) + blockIdx.x] = (uint8_t)(Y + 127);
       }
     }
   }
-  if (ROUTED) publish_routes(a, s_inds, s_w, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, tid);
+  if (ROUTED && blockIdx.x == 0 && blockIdx.y == 0) {   // block (0, 0) publishes the full routing for the down kernel
+    if (fast) {
+      __syncthreads();
+      full_routing(a, sel, s_inds, s_w, lurows, luw, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, wave);
+    }
+    publish_routes(a, s_inds, s_w, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, tid);
+  }
 }
 
 // ------------------------------------------------------------------ Kernel B + combine (owner computes)
@@ -516,19 +543,26 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
       a.part[(size_t)ur * a.H + m0 + mi] = d * cuw[ur];
     }
   }
+  // combine: every (route, output) term d * w in parallel, then each output adds its k terms in route order
   const uint32_t nrows = (uint32_t)(U * a.R);
-  for (int e = tid; e < a.M * 16; e += blockDim.x) {
-    const int row = e >> 4, mi = e & 15;
-    float accy = 0.0f;
-    for (int j = 0; j < a.k; ++j) {
-      const uint32_t idx = cgidx[row * a.k + j];
-      const int pr = idx < nrows ? route_row(idx) : -1;
-      if (pr >= 0) {
-        float d = part[pr * 16 + mi] + part[(nr + pr) * 16 + mi];
-        if (a.round_bf16) d = round_bf16(d);
-        accy = accy + d * cuw[idx];
-      }
+  __shared__ float cterm[1024];       // [M * k][16], M * k <= 64
+  if (tid < nr * 16) {
+    const int t = tid >> 4, mi = tid & 15;
+    const uint32_t idx = cgidx[t];
+    const int pr = idx < nrows ? route_row(idx) : -1;
+    float term = 0.0f;
+    if (pr >= 0) {
+      float d = part[pr * 16 + mi] + part[(nr + pr) * 16 + mi];
+      if (a.round_bf16) d = round_bf16(d);
+      term = d * cuw[idx];
     }
+    cterm[tid] = term;
+  }
+  __syncthreads();
+  if (tid < a.M * 16) {
+    const int row = tid >> 4, mi = tid & 15;
+    float accy = 0.0f;
+    for (int j = 0; j < a.k; ++j) accy = accy + cterm[(row * a.k + j) * 16 + mi];
     a.y[(size_t)row * a.H + m0 + mi] = f32_to_bf16(accy);
   }
 }
@@ -747,7 +781,7 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
   hipStream_t st = as_stream(stream);
 
   RouterSmallArgs ra{};
-  ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = M; ra.H = H; ra.E = E; ra.k = k; ra.nlog = (E + 3) / 4;
+  ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = M; ra.H = H; ra.E = E; ra.k = k;
   ra.logits = logits; ra.scores = scores; ra.keys = keys;
   ra.xq_hi = ew.xq_hi; ra.xq_lo = ew.xq_lo; ra.xq_hs = ew.xq_hs; ra.xq_ls = ew.xq_ls;
   rc = launch_router_logits_small(ra, st);

@@ -192,6 +192,25 @@ __device__ __forceinline__ float dpp_group_max8(float v) {
   return v;
 }
 
+// max over each group of 16 consecutive lanes (a DPP row): the 8-lane steps, then the row mirror
+__device__ __forceinline__ float dpp_group_max16(float v) {
+  v = dpp_group_max8(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
+// wave64 sum through DPP row operations (xor 1, xor 2, half-row and row mirrors, then row_bcast15 / 31 into
+// rows 1-3); the total is read from lane 63 and returned to every lane
+__device__ __forceinline__ float dpp_sum_f32(float v) {
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // wave64 max / min of a uint32 through DPP row operations (xor 1, xor 2, half-row and row mirrors, then the
 // row_bcast15 / row_bcast31 steps across rows); every lane receives the result read from lane 63.
 __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {

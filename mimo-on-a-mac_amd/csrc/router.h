@@ -9,7 +9,7 @@ struct RouterSmallArgs {
   const uint16_t* x;       // [T, H] bf16
   const uint16_t* Wg;      // [E, H] bf16
   const float* bias;       // [E]
-  int T, H, E, k, nlog;    // nlog = ceil(E / 4) logits blocks
+  int T, H, E, k, nlog;    // nlog = E logits blocks (set by the launcher)
   float* logits;           // [T, E]
   float* scores;           // [T, E] sigmoid
   float* keys;             // [T, E] sigmoid + bias

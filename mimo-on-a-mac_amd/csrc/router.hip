@@ -71,24 +71,30 @@ __device__ void block_group_routes(const int32_t* inds, const float* scores, con
 
 // ------------------------------------------------------------------ small-T router (T <= 8)
 // Two kernels, no cross-block synchronisation inside either:
-//  router_logits_small_kernel: blocks [0, nlog) give one wave per expert: T logits (fp32 FMA over bf16
-//    products, the expert's weight row loaded in one batch), then sigmoid and key by one lane per row;
+//  router_logits_small_kernel: blocks [0, nlog = E) give one block per expert: T logits (fp32 FMA over bf16
+//    products; each wave a quarter of the row, loaded in one batch with the T activation rows, summed through
+//    DPP and then in LDS in a fixed order), then sigmoid and key by one thread per row;
 //    blocks [nlog, ...) split x into hi/lo E4M3 halves for the expert kernels (one thread per 32-block).
 //  router_select_group_kernel (one block): top-k per row (one wave per row) and the grouping by slot.
 template <int NCH>
 __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if ((int)blockIdx.x >= a.nlog) {           // hi/lo split of x: one element per lane, 32 lanes per block
     if (!a.xq_hi) return;
     const int64_t n = (int64_t)a.T * a.H;
     const int64_t idx = ((int64_t)(blockIdx.x - a.nlog) * blockDim.x + threadIdx.x);
     const bool live = idx < n;
     const float v = live ? bf16_to_f32(a.x[idx]) : 0.0f;
-    const int X = fp8_block_exp(group_max(fabsf(v), 32));
+    float amax = dpp_group_max16(fabsf(v));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    const int X = fp8_block_exp(amax);
     float dec;
     const uint32_t hc = e4m3_encode(v, X, &dec);
     const float res = v - dec;
-    const int Y = fp8_block_exp(group_max(fabsf(res), 32));
+    float ramax = dpp_group_max16(fabsf(res));
+    ramax = fmaxf(ramax, __shfl_xor(ramax, 16, 64));
+    const int Y = fp8_block_exp(ramax);
     const uint32_t lc = e4m3_encode(res, Y, &dec);
     if (live) {
       a.xq_hi[idx] = (uint8_t)hc;
@@ -100,48 +106,55 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
     }
     return;
   }
-  const int e = blockIdx.x * 4 + wave;
-  if (e >= a.E) return;                          // wave-uniform; no block-level synchronisation below
-  // lane owns the 8-element chunks c*512 + lane*8 (c < NCH); chunks past H read element 0 and count 0
-  const uint16_t* wrow = a.Wg + (size_t)e * a.H;
-  uint4 wq[NCH];
+  // block e: expert e's logits for the T <= 8 rows.  Wave w covers elements [w H/4, (w+1) H/4): lane owns the
+  // 8-element chunks c*512 + lane*8 of that range (c < NCH; chunks past it read element 0 and count 0).
+  __shared__ float part[8][4];
+  const int e = blockIdx.x;
+  const int q4 = a.H / 4;
+  const uint16_t* wrow = a.Wg + (size_t)e * a.H + wave * q4;
+  uint4 wq[NCH], xq[8][NCH];
   bool ok[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int off = c * 512 + lane * 8;
-    ok[c] = off < a.H;
+    ok[c] = off < q4;
     wq[c] = *reinterpret_cast<const uint4*>(wrow + (ok[c] ? off : 0));
   }
-  __builtin_amdgcn_sched_barrier(0);
-  float mine = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const uint16_t* xrow = a.x + (size_t)(r < a.T ? r : 0) * a.H + wave * q4;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (r < a.T) xq[r][c] = *reinterpret_cast<const uint4*>(xrow + (ok[c] ? c * 512 + lane * 8 : 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);     // every load is in flight before the arithmetic
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     if (r < a.T) {
-      const uint16_t* xrow = a.x + (size_t)r * a.H;
-      uint4 xq[NCH];
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) xq[c] = *reinterpret_cast<const uint4*>(xrow + (ok[c] ? c * 512 + lane * 8 : 0));
-      float acc = 0.0f;
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains, added in a fixed order
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        const uint4 xv = ok[c] ? xq[c] : make_uint4(0, 0, 0, 0);
-        uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
-        uint32_t wp[4] = {wq[c].x, wq[c].y, wq[c].z, wq[c].w};
+        const uint4 xv = ok[c] ? xq[r][c] : make_uint4(0, 0, 0, 0);
+        const uint32_t xp[4] = {xv.x, xv.y, xv.z, xv.w};
+        const uint32_t wp[4] = {wq[c].x, wq[c].y, wq[c].z, wq[c].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          acc = fmaf(__uint_as_float(xp[j] << 16), __uint_as_float(wp[j] << 16), acc);
-          acc = fmaf(__uint_as_float(xp[j] & 0xFFFF0000u), __uint_as_float(wp[j] & 0xFFFF0000u), acc);
+          acc[j] = fmaf(__uint_as_float(xp[j] << 16), __uint_as_float(wp[j] << 16), acc[j]);
+          acc[j] = fmaf(__uint_as_float(xp[j] & 0xFFFF0000u), __uint_as_float(wp[j] & 0xFFFF0000u), acc[j]);
         }
       }
-      float l = wave_sum(acc);
-      if (lane == r) mine = l;
+      const float s = dpp_sum_f32((acc[0] + acc[1]) + (acc[2] + acc[3]));
+      if (lane == 0) part[r][wave] = s;
     }
   }
-  if (lane < a.T) {                 // one lane per row: sigmoid and selection key
-    float s = sigmoid_spec(mine);
-    a.logits[lane * a.E + e] = mine;
-    a.scores[lane * a.E + e] = s;
-    a.keys[lane * a.E + e] = s + a.bias[e];
+  __syncthreads();
+  if (threadIdx.x < a.T) {          // one thread per row: the four quarters in order, sigmoid and selection key
+    const int r = threadIdx.x;
+    const float l = ((part[r][0] + part[r][1]) + part[r][2]) + part[r][3];
+    const float s = sigmoid_spec(l);
+    a.logits[r * a.E + e] = l;
+    a.scores[r * a.E + e] = s;
+    a.keys[r * a.E + e] = s + a.bias[e];
   }
 }
 
@@ -381,13 +394,13 @@ size_t dispatch_workspace(int n, int n_slots) {
   return align256((size_t)nchunks * n_slots * sizeof(int32_t));
 }
 
-int launch_router_logits_small(const RouterSmallArgs& a, hipStream_t st) {
+int launch_router_logits_small(const RouterSmallArgs& args, hipStream_t st) {
+  RouterSmallArgs a = args;
   int nquant = a.xq_hi ? (int)(((int64_t)a.T * a.H + 255) / 256) : 0;
-  const int nch = (a.H + 511) / 512;
+  a.nlog = a.E;
+  const int nch = (a.H / 4 + 511) / 512;
   ProfScope p(st, "router_logits_small");
   switch (nch) {
-    case 8: router_logits_small_kernel<8><<<a.nlog + nquant, 256, 0, st>>>(a); break;
-    case 4: router_logits_small_kernel<4><<<a.nlog + nquant, 256, 0, st>>>(a); break;
     case 2: router_logits_small_kernel<2><<<a.nlog + nquant, 256, 0, st>>>(a); break;
     default: router_logits_small_kernel<1><<<a.nlog + nquant, 256, 0, st>>>(a); break;
   }

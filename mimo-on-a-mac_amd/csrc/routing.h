@@ -17,25 +17,12 @@ namespace mimo {
 // T plus the lowest-id keys equal to T; its k entries are then ranked by (key descending, id ascending) in
 // LDS.  Renormalisation sums the scores sequentially in that order.
 constexpr int kSelLds = 80;   // ints of LDS scratch per selecting wave (k <= 16)
+
+// The selected set of one row: take[j] says whether candidate lane + 64 j is among the top k (key order,
+// ties to the lower id).  cv: the order-preserving keys.
 template <int PER>
-__device__ __forceinline__ void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
-                                                  int32_t* inds_out, float* w_out, int* lds_sel) {
+__device__ __forceinline__ void wave_select_set(const uint32_t (&cv)[PER], int k, bool (&take)[PER]) {
   const int lane = threadIdx.x & 63;
-  uint32_t* t_key = reinterpret_cast<uint32_t*>(lds_sel);        // [16] selected, in (j, lane) order
-  int* t_id = lds_sel + 16;
-  float* t_sc = reinterpret_cast<float*>(lds_sel + 32);
-  int* f_id = lds_sel + 48;                                        // [16] in canonical order
-  float* f_sc = reinterpret_cast<float*>(lds_sel + 64);
-  uint32_t cv[PER];
-  float sc[PER], kv[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {            // every load in flight before any is used
-    const int e = lane + 64 * j;
-    kv[j] = key_row[e < E ? e : 0];
-    sc[j] = s_row[e < E ? e : 0];
-  }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) cv[j] = (lane + 64 * j) < E ? key_to_ordered(kv[j]) + 1u : 0u;
   // count(cv >= lo) >= k (every candidate has cv >= 1 and E >= k); count(cv >= hi) < k (cv < 2^32 - 1)
   uint32_t lo = 1u, hi = 0xFFFFFFFFu;
   while (hi - lo > 1u) {
@@ -52,19 +39,52 @@ __device__ __forceinline__ void wave_select_row_t(const float* s_row, const floa
 #pragma unroll
   for (int j = 0; j < PER; ++j) ngt += __popcll(__ballot(cv[j] > T));
   const int need = k - ngt;                  // keys equal to T that are taken, lowest ids first
-  int ties_before = 0, sel_before = 0;
+  int ties_before = 0;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint64_t tie = __ballot(cv[j] == T);
-    const bool take = cv[j] > T || (cv[j] == T && ties_before + __popcll(tie & below) < need);
-    const uint64_t sel = __ballot(take);
-    if (take) {
+    take[j] = cv[j] > T || (cv[j] == T && ties_before + __popcll(tie & below) < need);
+    ties_before += __popcll(tie);
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void wave_load_keys(const float* key_row, int E, uint32_t (&cv)[PER]) {
+  const int lane = threadIdx.x & 63;
+  float kv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) kv[j] = key_row[(lane + 64 * j) < E ? lane + 64 * j : 0];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) cv[j] = (lane + 64 * j) < E ? key_to_ordered(kv[j]) + 1u : 0u;
+}
+
+template <int PER>
+__device__ __forceinline__ void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
+                                                  int32_t* inds_out, float* w_out, int* lds_sel) {
+  const int lane = threadIdx.x & 63;
+  uint32_t* t_key = reinterpret_cast<uint32_t*>(lds_sel);        // [16] selected, in (j, lane) order
+  int* t_id = lds_sel + 16;
+  float* t_sc = reinterpret_cast<float*>(lds_sel + 32);
+  int* f_id = lds_sel + 48;                                        // [16] in canonical order
+  float* f_sc = reinterpret_cast<float*>(lds_sel + 64);
+  uint32_t cv[PER];
+  float sc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sc[j] = s_row[(lane + 64 * j) < E ? lane + 64 * j : 0];   // with the keys below
+  wave_load_keys<PER>(key_row, E, cv);
+  bool take[PER];
+  wave_select_set<PER>(cv, k, take);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int sel_before = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint64_t sel = __ballot(take[j]);
+    if (take[j]) {
       const int pos = sel_before + __popcll(sel & below);
       t_key[pos] = cv[j];
       t_id[pos] = lane + 64 * j;
       t_sc[pos] = sc[j];
     }
-    ties_before += __popcll(tie);
     sel_before += __popcll(sel);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
