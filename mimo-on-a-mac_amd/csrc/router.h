@@ -40,7 +40,7 @@ int launch_router_select(const float* logits, const float* bias, int T, int E, i
                          float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
                          hipStream_t st);
 int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
-                    int32_t* inv, int tile_rows, int32_t* tile_off, int32_t* status, hipStream_t st);
+                    int32_t* inv, int tile_rows, int32_t* tile_off, int4* tiles, int32_t* status, hipStream_t st);
 size_t dispatch_workspace(int n, int n_slots);
 int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint8_t* hi, uint8_t* hs, uint8_t* lo,
                              uint8_t* ls, hipStream_t st);

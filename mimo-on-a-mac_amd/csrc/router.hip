@@ -308,10 +308,11 @@ __global__ void __launch_bounds__(1024) dispatch_hist_kernel(const int32_t* __re
 }
 
 // offsets[s] = exclusive scan of per-slot totals; base[b][s] = offsets[s] + sum_{b' < b} hist[b'][s];
-// tile_off[s] = exclusive scan of ceil(count[s] / tile_rows) (row tiles of the grouped GEMM).
+// tile_off[s] = exclusive scan of ceil(count[s] / tile_rows) (row tiles of the grouped GEMM); tiles[t] =
+// (slot, first sorted route, end route, 0) of row tile t.
 __global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int n_slots,
                                                              int32_t* __restrict__ offsets, int tile_rows,
-                                                             int32_t* __restrict__ tile_off) {
+                                                             int32_t* __restrict__ tile_off, int4* __restrict__ tiles) {
   extern __shared__ int sh[];
   int* tot = sh;
   int* til = sh + n_slots;
@@ -338,6 +339,14 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict
   for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
     offsets[s] = tot[s];
     if (tile_off) tile_off[s] = til[s];
+    if (tiles) {
+      const int end = s + 1 < n_slots ? tot[s + 1] : offsets[n_slots];
+      const int t1 = s + 1 < n_slots ? til[s + 1] : tile_off[n_slots];
+      for (int t = til[s]; t < t1; ++t) {
+        const int b = tot[s] + (t - til[s]) * tile_rows;
+        tiles[t] = make_int4(s, b, b + tile_rows < end ? b + tile_rows : end, 0);
+      }
+    }
     int acc = tot[s];
     for (int b = 0; b < nchunks; ++b) {
       int c = hist[(size_t)b * n_slots + s];
@@ -376,13 +385,13 @@ __global__ void __launch_bounds__(1024) dispatch_place_kernel(const int32_t* __r
 }
 
 int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
-                    int32_t* inv, int tile_rows, int32_t* tile_off, int32_t* status, hipStream_t st) {
+                    int32_t* inv, int tile_rows, int32_t* tile_off, int4* tiles, int32_t* status, hipStream_t st) {
   int nchunks = (n + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK;
   if (nchunks == 0) nchunks = 1;
   ProfScope p(st, "prefill_dispatch");
   dispatch_hist_kernel<<<nchunks, 1024, n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, status);
   dispatch_scan_kernel<<<1, 1024, 2 * n_slots * sizeof(int), st>>>(hist, nchunks, n_slots, offsets, tile_rows,
-                                                                     tile_off);
+                                                                     tile_off, tiles);
   if (n > 0)
     dispatch_place_kernel<<<nchunks, 1024, 16 * n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, perm, inv);
   return check_launch("prefill dispatch");
@@ -476,7 +485,7 @@ int mimo_prefill_dispatch(const int32_t* slot_inds, int T, int k, int n_slots, i
                "prefill_dispatch: need 1 <= n_slots <= 1024");
   MIMO_REQUIRE(ws && ws_bytes >= dispatch_workspace(T * k, n_slots), MIMO_ERR_WORKSPACE,
                "prefill_dispatch: workspace too small");
-  return launch_dispatch(slot_inds, T * k, n_slots, static_cast<int32_t*>(ws), perm, offsets, inv, 0, nullptr,
+  return launch_dispatch(slot_inds, T * k, n_slots, static_cast<int32_t*>(ws), perm, offsets, inv, 0, nullptr, nullptr,
                          nullptr, as_stream(stream));
 }
 
