@@ -14,6 +14,10 @@ and 4 rows, and the per-kernel durations measured with HIP events.  "cpu_baselin
 (the CPU restatement of the reference algorithm) on a bounded sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 500] [--warmup 20]
+
+HBM traffic of the dominant kernel (the "traffic" field of "roofline") comes from two rocprofv3 counter runs
+of `python bench.py --traffic-run` (FETCH_SIZE, then WRITE_SIZE), reduced by `--traffic-parse` against a
+plain elementwise copy of known size measured in the same runs; the result is committed under profiles/.
 """
 import argparse
 import json
@@ -48,6 +52,11 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="profiling payload: a 1 GiB calibration copy, then 1-row decode steps over 8 layers")
+    ap.add_argument("--traffic-parse", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="reduce two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --traffic-run to "
+                         "profiles/traffic.json")
     return ap.parse_args()
 
 
@@ -288,8 +297,94 @@ def _cpu_model():
     return "unknown CPU"
 
 
+CALIB_BYTES = 1 << 30        # the calibration copy reads and writes this many bytes
+
+
+def traffic_run():
+    """Workload for the counter runs: the calibration copy (an elementwise multiply by one over 1 GiB, so a
+    kernel, not a DMA copy), then 24 one-row decode steps rotating over 8 resident layers (8 x 103 MB, more
+    than the 256 MB MALL holds)."""
+    import numpy as np
+    import torch
+    src = torch.ones(CALIB_BYTES // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    layers = Layers(8, "cuda")
+    rng = np.random.default_rng(5)
+    xs = [torch.from_numpy(steered_rows(rng, layers.W[l % 8], controlled_sets(rng, 1))).to(torch.bfloat16).cuda()
+          for l in range(24)]
+    for s in range(24):
+        layers.blocks[s % 8](xs[s])
+    torch.cuda.synchronize()
+    log("[traffic] done")
+
+
+def _counter_rows(d):
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            rows += list(csv.DictReader(f))
+    if not rows:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    return rows
+
+
+def traffic_parse(fetch_dir, write_dir):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) averaged per kernel; each scaled by bytes / counter of the
+    calibration copy.  Writes profiles/traffic.json and prints a markdown summary."""
+    def per_kernel(d, counter):
+        acc = {}
+        for r in _counter_rows(d):
+            if r.get("Counter_Name") != counter:
+                continue
+            acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) * 1024.0)
+        return acc
+    f = per_kernel(fetch_dir, "FETCH_SIZE")
+    w = per_kernel(write_dir, "WRITE_SIZE")
+    def pick(acc, key):
+        names = [n for n in acc if key(n)]
+        if not names:
+            raise SystemExit(f"kernel not found among {sorted(acc)[:20]}")
+        vals = [v for n in names for v in acc[n]]
+        return names[0], vals
+    cal = lambda n: "elementwise" in n and "Mul" in n
+    gu = lambda n: "decode_gateup_kernel" in n
+    _, cf = pick(f, cal)
+    _, cw = pick(w, cal)
+    fetch_scale = CALIB_BYTES / (sum(cf) / len(cf))
+    write_scale = CALIB_BYTES / (sum(cw) / len(cw))
+    name, gf = pick(f, gu)
+    _, gw = pick(w, gu)
+    fetch = sum(gf) / len(gf) * fetch_scale
+    write = sum(gw) / len(gw) * write_scale
+    algo = 8 * GATEUP_BYTES_PER_EXPERT
+    out = {"decode_gateup_kernel:decode_m1": fetch + write,
+           "_detail": {"kernel": name, "dispatches": len(gf), "fetch_bytes": fetch, "write_bytes": write,
+                       "algorithmic_bytes": algo, "fetch_scale": fetch_scale, "write_scale": write_scale,
+                       "calibration": "elementwise multiply by one over 1 GiB: reads and writes 1 GiB"}}
+    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(f"| kernel | dispatches | FETCH (MB/launch) | WRITE (MB/launch) | algorithmic (MB/launch) | fetch / algorithmic |")
+    print(f"|---|---|---|---|---|---|")
+    print(f"| decode_gateup_kernel (1 row, 8 experts) | {len(gf)} | {fetch / 1e6:.2f} | {write / 1e6:.3f} | "
+          f"{algo / 1e6:.2f} | {fetch / algo:.3f} |")
+    print(f"\ncalibration: FETCH_SIZE scale {fetch_scale:.4f}, WRITE_SIZE scale {write_scale:.4f} (bytes per counted "
+          f"byte, from the 1 GiB elementwise copy)")
+
+
 def main():
     args = parse()
+    if args.traffic_parse:
+        traffic_parse(*args.traffic_parse)
+        return
+    if args.traffic_run:
+        traffic_run()
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only: the MoE block runs on a single MI355X "

@@ -152,8 +152,9 @@ size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, i
 /* ---------------------------------------------------------------- measurement */
 
 /* No counterpart in the reference: per-kernel timing for benchmarks.  While enabled, every kernel launch is
- * bracketed by HIP events on its stream (adds one event record per launch).  mimo_profile_enable also clears
- * the records.  mimo_profile_read synchronises on the recorded events and returns the number of distinct
+ * followed by a HIP event on its stream; the kernel's time runs from the previous kernel's event of the same
+ * entry-point call (or from an event recorded just before it, for the first kernel of a call) to its own, so
+ * back-to-back kernels add one event record each.  mimo_profile_enable also clears the records.  mimo_profile_read synchronises on the recorded events and returns the number of distinct
  * kernel names; for the first max_kernels of them it writes the name (64 bytes each, NUL-terminated, host
  * buffer), the total milliseconds and the launch count (host arrays). */
 int mimo_profile_enable(int on);

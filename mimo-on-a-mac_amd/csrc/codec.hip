@@ -27,6 +27,7 @@ void clear_error() { g_err.clear(); }
 struct ProfRec {
   const char* name;
   hipEvent_t a, b;
+  bool owns_a;          // false when a is the previous record's end event (chained)
 };
 static std::mutex g_prof_mu;
 static bool g_prof_on = false;
@@ -34,6 +35,12 @@ static std::vector<ProfRec> g_prof;
 static std::vector<hipEvent_t> g_prof_pool;
 static const char* g_prof_open = nullptr;
 static hipEvent_t g_prof_open_ev;
+static bool g_prof_open_owns = true;
+// Within one multi-kernel entry point (ProfChain), a kernel's begin is the previous kernel's end event on the
+// same stream: one event per launch, so the timing adds no begin packet of its own.
+static int g_prof_chain = 0;
+static hipEvent_t g_prof_last_end = nullptr;
+static hipStream_t g_prof_last_stream = nullptr;
 
 static hipEvent_t prof_event() {
   if (!g_prof_pool.empty()) {
@@ -49,11 +56,18 @@ static hipEvent_t prof_event() {
 void prof_begin(hipStream_t st, const char* name) {
   if (!g_prof_on) return;
   std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (g_prof_chain && g_prof_last_end && g_prof_last_stream == st) {
+    g_prof_open = name;
+    g_prof_open_ev = g_prof_last_end;
+    g_prof_open_owns = false;
+    return;
+  }
   hipEvent_t e = prof_event();
   if (!e) return;
   hipEventRecord(e, st);
   g_prof_open = name;
   g_prof_open_ev = e;
+  g_prof_open_owns = true;
 }
 
 void prof_end(hipStream_t st) {
@@ -63,8 +77,17 @@ void prof_end(hipStream_t st) {
   hipEvent_t e = prof_event();
   if (!e) return;
   hipEventRecord(e, st);
-  g_prof.push_back({g_prof_open, g_prof_open_ev, e});
+  g_prof.push_back({g_prof_open, g_prof_open_ev, e, g_prof_open_owns});
   g_prof_open = nullptr;
+  g_prof_last_end = e;
+  g_prof_last_stream = st;
+}
+
+void prof_chain(bool on) {
+  if (!g_prof_on) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_chain += on ? 1 : -1;
+  if (on && g_prof_chain == 1) g_prof_last_end = nullptr;     // the chain starts with a fresh begin event
 }
 
 // ------------------------------------------------------------------ seeded normal generator
@@ -263,9 +286,14 @@ int mimo_abi_version(void) { return MIMO_ABI_VERSION; }
 
 int mimo_profile_enable(int on) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
-  for (auto& r : g_prof) { g_prof_pool.push_back(r.a); g_prof_pool.push_back(r.b); }
+  for (auto& r : g_prof) {
+    if (r.owns_a) g_prof_pool.push_back(r.a);
+    g_prof_pool.push_back(r.b);
+  }
   g_prof.clear();
   g_prof_open = nullptr;
+  g_prof_last_end = nullptr;
+  g_prof_chain = 0;
   g_prof_on = on != 0;
   return MIMO_OK;
 }

@@ -698,6 +698,7 @@ int mimo_moe_experts(const uint16_t* x, int M, const mimo_bank* bank, const int3
                      const int32_t* ucnt, const float* uw, const int32_t* n_unique, int Umax, int R,
                      const uint32_t* gidx, int k, int round_expert_bf16, uint16_t* y, uint16_t* h_out,
                      float* part_out, void* ws, size_t ws_bytes, void* stream) {
+  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && uslot && urows && ucnt && uw && gidx && y, MIMO_ERR_ARG, "moe_experts: null pointer");
@@ -761,6 +762,7 @@ size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
 int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
                     int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
                     size_t ws_bytes, void* stream) {
+  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_decode: null pointer");

@@ -27,6 +27,12 @@ inline int check_launch(const char* what) {
 // HIP events on the launch stream; mimo_profile_read aggregates durations per kernel name.
 void prof_begin(hipStream_t st, const char* name);
 void prof_end(hipStream_t st);
+void prof_chain(bool on);
+// Multi-kernel entry points time their kernels back to back: each begin is the previous kernel's end event.
+struct ProfChain {
+  ProfChain() { prof_chain(true); }
+  ~ProfChain() { prof_chain(false); }
+};
 struct ProfScope {
   hipStream_t st;
   ProfScope(hipStream_t s, const char* name) : st(s) { prof_begin(s, name); }

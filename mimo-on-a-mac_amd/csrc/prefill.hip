@@ -400,6 +400,7 @@ size_t mimo_moe_prefill_workspace_size(int T, int k, int n_slots, int H, int I) 
 
 int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* w, int k, const mimo_bank* bank,
                      uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
+  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
   int rc = check_prefill_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && slot_inds && w && y, MIMO_ERR_ARG, "moe_prefill: null pointer");
@@ -421,6 +422,7 @@ size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, i
 int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
                            int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
                            size_t ws_bytes, void* stream) {
+  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
   int rc = check_prefill_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_prefill_block: null pointer");
