@@ -20,8 +20,9 @@ namespace mimo {
 
 struct PrefillArgs {
   const uint8_t *xq_hi, *xq_lo, *xq_hs, *xq_ls;   // [T, H], [T, H/32]
-  const int32_t *perm, *offsets, *tile_off, *inv;
-  const int4* tiles;                              // (slot, first route, end route, 0) per row tile
+  const int32_t *perm, *offsets, *inv;
+  const int4* tiles;      // [0] = (wide tiles, narrow tiles); wide at 1 + t, narrow at 1 + wcap + t: (slot, beg, end, 0)
+  int wcap;
   const float* w;
   int T, k, S, H, I, P;
   const uint32_t *gate_w, *up_w, *down_w;
@@ -32,145 +33,206 @@ struct PrefillArgs {
   uint16_t* y;                                    // [T, H]
 };
 
-constexpr int PF_ROWS = 64;        // routes per row tile
-constexpr int PF_STAGES = 4;
-// Per-stage LDS layout (bytes).  A: two planes (hi, lo) of 64 routes x 128 codes, the 16-byte chunk q of route
-// r stored at slot q ^ (r & 7); the lo plane starts 128 bytes off the hi plane's bank phase.  B: 256 weight
-// rows x 64 bytes, chunk g of row r at slot (g + (r & 15) / 4) & 3.  Both layouts make the MFMA operand
-// reads conflict-free.
-constexpr int PF_A_LO = 8192 + 128;
-constexpr int PF_B = 16640;
-constexpr int PF_AS = PF_B + 16384;       // [2 planes][64 routes] scale words (4 K-blocks)
-constexpr int PF_BS = PF_AS + 512;        // [256 rows] scale words
-constexpr int PF_DUMMY = PF_BS + 1024;    // target of the copies that keep every wave's count equal
-constexpr int PF_STAGE = PF_DUMMY + 256;  // 34816
-constexpr int PF_LDS = PF_STAGES * PF_STAGE;
-constexpr int PF_COPIES = 5;              // global -> LDS copies per wave and stage
+// Row tiles.  The dispatch cuts each slot's sorted routes into tiles of one of two shapes:
+//   narrow: a slot with at most 32 routes (4 chunks of 8) is one tile, multiplied by 512 weight rows per block
+//           (gate/up: 256 outputs of each projection; down: 512 outputs).  These blocks stream weights at the
+//           HBM rate with little MFMA work, so the wider weight tile halves their activation re-reads.
+//   wide:   a larger slot is split into ceil(count / 96) tiles of near-equal whole 8-route chunks (at most 12),
+//           multiplied by 256 weight rows per block (128 + 128 outputs, or 256 down outputs).
+// Both shapes stage 40 KB per K-step of 128 through a 3-slot LDS ring: the hi and lo activation code planes of
+// the tile's routes and the block's E2M1 weight rows.  The E8M0 scales of 8 K-steps (32 bytes per row) are
+// copied at once into one of two epoch buffers, one 4-byte word per lane, so scale traffic costs one request
+// per row every 8 steps.
+constexpr int PF_NARROW_MAX = 32;
+constexpr int PF_WIDE_ROWS = 96;
+constexpr int PF_STAGES = 3;                         // one step multiplied while two are in flight
+constexpr int PF_STAGE = 41216;
+constexpr int PF_EPOCH = 8;                          // K-steps per scale copy
+constexpr int PF_SC = PF_STAGES * PF_STAGE;          // the two epoch buffers follow the ring
+constexpr int PF_SC_BYTES = 18432;                   // 576 rows x 32 bytes (narrow: 64 A rows + 512 B rows)
+constexpr int PF_LDS = PF_SC + 2 * PF_SC_BYTES;      // 160512 bytes
 
-__device__ __forceinline__ void wait_vm_le(int n) {   // s_waitcnt vmcnt(n), n in {0, 5, 10}
-  if (n >= 10) __builtin_amdgcn_s_waitcnt(0x0F7A);
+// Stage layout: A planes of R routes x 128 codes, the 16-byte chunk q of route r at slot q ^ (r & 7), the lo
+// plane 128 bytes off the hi plane's bank phase; B rows of 64 bytes, chunk g of row r at slot (g + (r & 15) / 4)
+// & 3.  Both make the MFMA operand reads conflict-free.  Copies per wave: ACOP + BCOP per K-step (5 in both
+// shapes), ECOP per epoch.  A wave multiplies 4 weight tiles (64 rows) by NJ chunks spaced CSTEP apart.
+template <bool WIDE> struct PfShape;
+template <> struct PfShape<false> {
+  static constexpr int R = 32, NCH = 4, N = 512, A_PL = 4224, B_OFF = 8448;
+  static constexpr int ACOP = 1, BCOP = 4, ECOP = 9, NJ = 4, CSTEP = 1;
+};
+template <> struct PfShape<true> {
+  static constexpr int R = 96, NCH = 12, N = 256, A_PL = 12416, B_OFF = 24832;
+  static constexpr int ACOP = 3, BCOP = 2, ECOP = 7, NJ = 6, CSTEP = 2;
+};
+
+// s_waitcnt vmcnt(n) for the counts of the K loop (0, 5, 5 + 7, 5 + 9); a smaller count only waits longer
+__device__ __forceinline__ void pf_wait(int n) {
+  if (n >= 14) __builtin_amdgcn_s_waitcnt(0x0F7E);
+  else if (n >= 12) __builtin_amdgcn_s_waitcnt(0x0F7C);
   else if (n >= 5) __builtin_amdgcn_s_waitcnt(0x0F75);
   else __builtin_amdgcn_s_waitcnt(0x0F70);
 }
+// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N).  Row q keeps its eight K-step words at positions
+// k ^ swz(q), so the scale reads of one MFMA (16 rows) fall in distinct banks.
+template <int R> __device__ __forceinline__ int pf_swz(int q) {
+  return ((q >> 2) ^ ((q >= R && q < 2 * R) ? 2 : 0)) & 3;
+}
 #define PF_MFMA(A, B, C, SA, SB) __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 0, 4, 0, (SA), 0, (SB))
-__device__ __forceinline__ uint32_t pf_byte(uint32_t w, int g) { return (w >> (8 * g)) & 0xFFu; }
 
-// GATEUP: A = the routes' token activations, B = gate rows 0-127 and up rows 128-255 of the block's outputs;
-// epilogue SwiGLU and the hi/lo split of h.  !GATEUP: A = the routes' h rows, B = down rows of 256 outputs;
-// epilogue bf16 expert outputs.
-template <bool GATEUP>
-__global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
-  extern __shared__ __align__(256) uint8_t pl[];
-  __shared__ int s_tok[PF_ROWS];
-  // XCD-aware order: workgroups go to the 8 XCDs round robin, so hardware block b runs on XCD b % 8.  XCD x
-  // takes the contiguous range [x * per, (x + 1) * per) of the used (tile, output block) pairs, output blocks
-  // fastest: a tile's activation rows and an expert's weights are then re-read from that XCD's L2.
-  const int ntiles = a.tile_off[a.S];
-  const int nblk = GATEUP ? a.I / 128 : a.H / 256;   // output blocks per tile
-  const int used = ntiles * nblk;
-  const int per = (used + 7) / 8;                    // the 1-D grid has at least 8 * per blocks
-  const int hw = blockIdx.x;
-  const int xcd = hw & 7, j = hw >> 3;
-  const int logical = xcd * per + j;
-  if (j >= per || logical >= used) return;
-  const int tile = logical / nblk;
-  const int4 tt = a.tiles[tile];
+// One (row tile, output block).  GATEUP: A = the routes' token activations, B = gate rows [0, N/2) and up rows
+// [N/2, N) of the block's N/2 outputs; epilogue SwiGLU and the hi/lo split of h.  !GATEUP: A = the routes' h
+// rows, B = down rows of N outputs; epilogue bf16 expert outputs.
+template <bool GATEUP, bool WIDE>
+__device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* s_tok, int slot, int beg, int nvalid,
+                                        int ob) {
+  using Sh = PfShape<WIDE>;
+  constexpr int R = Sh::R, N = Sh::N, NJ = Sh::NJ;
+  constexpr int HALF = GATEUP ? N / 2 : N;       // block rows of one projection
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int slot = __builtin_amdgcn_readfirstlane(tt.x);
-  const int beg = __builtin_amdgcn_readfirstlane(tt.y);
-  const int nvalid = __builtin_amdgcn_readfirstlane(tt.z) - beg;
-  const int K = GATEUP ? a.H : a.I;             // reduction length
+  const int K = GATEUP ? a.H : a.I;              // reduction length
   const int nK = K / 128;
-  const int ncol = GATEUP ? a.I : a.H;          // weight rows per slot
-  const int n0 = (logical - tile * nblk) * (GATEUP ? 128 : 256);
-  // activation row of each route (padding routes repeat the tile's first route)
-  if (tid < PF_ROWS) {
+  const int KS = K / 32;                         // scale bytes per row
+  const int ncol = GATEUP ? a.I : a.H;           // weight rows per slot and projection
+  const int n0 = ob * HALF;                      // first output of the block
+  // activation row of each route (padding routes repeat the tile's last route)
+  if (tid < R) {
     const int p = beg + min(tid, nvalid - 1);
     s_tok[tid] = GATEUP ? a.perm[p] / a.k : p;
   }
   __syncthreads();
-  const bool a_pad = 8 * wave + (lane >> 3) >= nvalid;   // this lane copies a padding route
   const uint8_t* a_hi = GATEUP ? a.xq_hi : a.hq_hi;
   const uint8_t* a_lo = GATEUP ? a.xq_lo : a.hq_lo;
   const uint8_t* a_hs = GATEUP ? a.xq_hs : a.hq_hs;
   const uint8_t* a_ls = GATEUP ? a.xq_ls : a.hq_ls;
-  // this wave's copies: A planes (routes 8w .. 8w+7), B rows 32w .. 32w+31, one scale or dummy row of 64 words
-  const int ar = 8 * wave + (lane >> 3);
-  // padding lanes all read the same 16 bytes (their rows are never used)
-  const uint32_t a_off = a_pad ? (uint32_t)s_tok[0] * (uint32_t)K
-                               : (uint32_t)s_tok[ar] * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
-  const bool up_half = GATEUP && wave >= 4;     // B rows 128-255 are the up projection
+  // A copies: 8-route block b = ACOP wave + c of plane b / NCH; padding lanes all read the same 16 bytes
+  // (bases and LDS offsets are chosen here, once: the copy loops below index these arrays with constants only)
+  uint32_t a_off[Sh::ACOP];
+  const uint8_t* a_src[Sh::ACOP];
+  int a_dst[Sh::ACOP];
+#pragma unroll
+  for (int c = 0; c < Sh::ACOP; ++c) {
+    const int b = Sh::ACOP * wave + c;
+    const int r = 8 * (b % Sh::NCH) + (lane >> 3);
+    a_off[c] = r < nvalid ? (uint32_t)s_tok[r] * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (r & 7))
+                          : (uint32_t)s_tok[0] * (uint32_t)K;
+    a_src[c] = b >= Sh::NCH ? a_lo : a_hi;
+    a_dst[c] = (b >= Sh::NCH ? Sh::A_PL : 0) + 1024 * (b % Sh::NCH);
+  }
+  // B copies: block rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding chunk (slot - row / 4) & 3
+  const bool up_half = GATEUP && wave >= 4;
   const uint32_t* bw = GATEUP ? (up_half ? a.up_w : a.gate_w) : a.down_w;
   const uint8_t* bw_base = reinterpret_cast<const uint8_t*>(bw) + ((size_t)slot * ncol + n0) * (K / 2);
-  const int brow0 = 32 * wave - (up_half ? 128 : 0);   // first weight row of the wave's copies in its projection
-  const uint32_t b_off0 = (uint32_t)(brow0 + (lane >> 2)) * (uint32_t)(K / 2) + 16u * (uint32_t)(((lane & 3) - (lane >> 4)) & 3);
-  const uint32_t b_off1 = b_off0 + 16u * (uint32_t)(K / 2);
-  // scale copies: wave 0 A hi, wave 1 A lo, waves 2-5 B rows 64 (w - 2) .. + 63, waves 6-7 a dummy repeat of wave 0's
-  const uint8_t* sc_base;
-  uint32_t sc_off;
-  int sc_dst;
-  if (wave < 2 || wave >= 6) {
-    sc_base = (wave == 1) ? a_ls : a_hs;
-    sc_off = (uint32_t)s_tok[lane < nvalid ? lane : 0] * (uint32_t)(K / 32);
-    sc_dst = wave == 0 ? PF_AS : (wave == 1 ? PF_AS + 256 : PF_DUMMY);
-  } else {
-    const int r = 64 * (wave - 2) + lane;          // B row of the block, 0..255
-    const bool up_r = GATEUP && r >= 128;
-    const uint8_t* s_pool = GATEUP ? (up_r ? a.up_s : a.gate_s) : a.down_s;
-    sc_base = s_pool + ((size_t)slot * ncol + n0) * (K / 32);
-    sc_off = (uint32_t)(r - (up_r ? 128 : 0)) * (uint32_t)(K / 32);
-    sc_dst = PF_BS + 256 * (wave - 2);
+  const int brow_c = (N / 8) * wave;
+  const uint32_t b_off = (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 2)) * (uint32_t)(K / 2) +
+                         16u * (uint32_t)(((lane & 3) - (lane >> 4)) & 3);
+  // scale copies: copy c covers epoch rows 8 (ECOP wave + c) .. + 7, eight lanes per row
+  const uint8_t* bs_base = (GATEUP ? a.gate_s : a.down_s) + ((size_t)slot * ncol + n0) * KS;
+  const uint8_t* us_base = a.up_s + ((size_t)slot * ncol + n0) * KS;
+  uint32_t e_off[Sh::ECOP], e_k4[Sh::ECOP];
+  const uint8_t* e_src[Sh::ECOP];
+#pragma unroll
+  for (int c = 0; c < Sh::ECOP; ++c) {
+    const int q0 = 8 * (Sh::ECOP * wave + c);
+    e_src[c] = q0 < R ? a_hs : q0 < 2 * R ? a_ls : (GATEUP && q0 - 2 * R >= HALF) ? us_base : bs_base;
+    // the lane's word position lane & 7 holds K-step (lane & 7) ^ swz(row) of the epoch
+    const int q = q0 + (lane >> 3);
+    e_k4[c] = 4u * (uint32_t)((lane & 7) ^ pf_swz<R>(q));
+    if (q < 2 * R) {
+      const int r = q < R ? q : q - R;
+      e_off[c] = (uint32_t)s_tok[r < nvalid ? r : 0] * (uint32_t)KS;
+    } else {
+      const int br = q - 2 * R;
+      e_off[c] = (uint32_t)(br - ((GATEUP && br >= HALF) ? HALF : 0)) * (uint32_t)KS;
+    }
   }
-  auto issue = [&](int s) {                        // the five copies of K-step s into ring slot s % 4
-    uint8_t* st = pl + (s & 3) * PF_STAGE;
-    const uint32_t k0 = (uint32_t)s * 128u;
-    lds_copy16(a_hi, a_off + k0, st + 1024 * wave);
-    lds_copy16(a_lo, a_off + k0, st + PF_A_LO + 1024 * wave);
-    lds_copy16(bw_base, b_off0 + k0 / 2, st + PF_B + 2048 * wave);
-    lds_copy16(bw_base, b_off1 + k0 / 2, st + PF_B + 2048 * wave + 1024);
-    lds_copy4(sc_base, sc_off + k0 / 32, st + sc_dst);
-  };
-  const int rh = wave & 1, ng = wave >> 1;
-  v4f acc[4][4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[c][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  // weight tile t of this wave: GATEUP t = 2 p + b (p gate/up, b 16-output half), else t = 16-output quarter
-  int brow[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) brow[t] = GATEUP ? (t >> 1) * 128 + 32 * ng + 16 * (t & 1) + i : 64 * ng + 16 * t + i;
-  const int bslot = 16 * ((g + (i >> 2)) & 3);
-  int nch = 0;                                     // active 8-route chunks of this wave
-#pragma unroll
-  for (int c = 0; c < 4; ++c) nch += (8 * (4 * rh + c) < nvalid) ? 1 : 0;
 
-  for (int s = 0; s < PF_STAGES - 1 && s < nK; ++s) issue(s);
+  auto issue_epoch = [&](int e) __attribute__((always_inline)) {
+    uint8_t* dst = pl + PF_SC + (e & 1) * PF_SC_BYTES;
+#pragma unroll
+    for (int c = 0; c < Sh::ECOP; ++c) {
+      // words past the row's end (K < 1024) read the row's first word instead; they are never used
+      const uint32_t kk = 32u * (uint32_t)e + e_k4[c];
+      lds_copy4(e_src[c], e_off[c] + (kk < (uint32_t)KS ? kk : 0u), dst + 256 * (Sh::ECOP * wave + c));
+    }
+  };
+  auto issue = [&](int s) __attribute__((always_inline)) {   // K-step s into ring slot s % 3 (and its epoch's scales)
+    if (s % PF_EPOCH == 0) issue_epoch(s / PF_EPOCH);
+    uint8_t* st = pl + (s % PF_STAGES) * PF_STAGE;
+    const uint32_t k0 = (uint32_t)s * 128u;
+#pragma unroll
+    for (int c = 0; c < Sh::ACOP; ++c) lds_copy16(a_src[c], a_off[c] + k0, st + a_dst[c]);
+#pragma unroll
+    for (int c = 0; c < Sh::BCOP; ++c)
+      lds_copy16(bw_base, b_off + (uint32_t)(16 * c) * (uint32_t)(K / 2) + k0 / 2u,
+                 st + Sh::B_OFF + 64 * (brow_c + 16 * c));
+  };
+
+  // the wave's tiles: weight rows 64 tg .. (GATEUP t = 2 p + b: projection p, 16-output half b), chunks
+  // cb + CSTEP j for j < nj
+  const int tg = WIDE ? (wave & 3) : wave;
+  const int cb = WIDE ? (wave >> 2) : 0;
+  uint32_t live = 0;                             // bit j: chunk cb + CSTEP j holds routes
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) live |= (8 * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
+  live = __builtin_amdgcn_readfirstlane(live);
+  int brow[4], bsc[4], bsw[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    brow[t] = GATEUP ? (t >> 1) * HALF + 32 * tg + 16 * (t & 1) + i : 64 * tg + 16 * t + i;
+    bsc[t] = 32 * (2 * R + brow[t]) + g;
+    bsw[t] = pf_swz<R>(2 * R + brow[t]);
+  }
+  const int bslot = 16 * ((g + (i >> 2)) & 3);
+  int aoff[NJ], asc[NJ], asw[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int r = 8 * (cb + Sh::CSTEP * j) + (i & 7);
+    const int q = (i >> 3) * R + r;
+    aoff[j] = (i >> 3) * Sh::A_PL + 128 * r;
+    asc[j] = 32 * q + g;
+    asw[j] = pf_swz<R>(q);
+  }
+  v4f acc[NJ][4];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[j][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  issue(0);
+  if (nK > 1) issue(1);
   for (int s = 0; s < nK; ++s) {
-    wait_vm_le(PF_COPIES * min(PF_STAGES - 2, nK - 1 - s));
-    __syncthreads();                               // step s landed everywhere; step s - 1 is no longer read
-    if (s + PF_STAGES - 1 < nK) issue(s + PF_STAGES - 1);
-    const uint8_t* st = pl + (s & 3) * PF_STAGE;
+    // copies issued after step s's: step s + 1's five, plus its epoch's scales when it opens one
+    pf_wait(s + 1 < nK ? 5 + (((s + 1) % PF_EPOCH == 0) ? Sh::ECOP : 0) : 0);
+    __syncthreads();                             // step s landed everywhere; step s - 1's slot is free
+    if (s + 2 < nK) issue(s + 2);
+    const uint8_t* st = pl + (s % PF_STAGES) * PF_STAGE;
+    const uint8_t* sc = pl + PF_SC + ((s / PF_EPOCH) & 1) * PF_SC_BYTES;
+    const int kw = s % PF_EPOCH;
     v8i B[4];
     int sb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const uint4 v = *reinterpret_cast<const uint4*>(st + PF_B + brow[t] * 64 + bslot);
+      const uint4 v = *reinterpret_cast<const uint4*>(st + Sh::B_OFF + brow[t] * 64 + bslot);
       B[t] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
-      sb[t] = (int)pf_byte(*reinterpret_cast<const uint32_t*>(st + PF_BS + 4 * brow[t]), g);
+      sb[t] = sc[bsc[t] + 4 * (kw ^ bsw[t])];
+    }
+    v8i A[NJ];
+    int sa[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {              // read unconditionally: fixed LDS counts let each MFMA group
+      const uint8_t* ab = st + aoff[j];         // wait for its own operands only
+      const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + 16 * (g ^ (i & 7)));
+      const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + 16 * ((4 + g) ^ (i & 7)));
+      A[j] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
+      sa[j] = sc[asc[j] + 4 * (kw ^ asw[j])];
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c < nch) {
-        const int r = 8 * (4 * rh + c) + (i & 7);
-        const uint8_t* ab = st + (i < 8 ? 0 : PF_A_LO) + 128 * r;
-        const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + 16 * (g ^ (i & 7)));
-        const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + 16 * ((4 + g) ^ (i & 7)));
-        const int sa = (int)pf_byte(*reinterpret_cast<const uint32_t*>(st + PF_AS + (i < 8 ? 0 : 256) + 4 * r), g);
-        const v8i A = {(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
+    for (int j = 0; j < NJ; ++j) {
+      if (live & (1u << j)) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[c][t] = PF_MFMA(A, B[t], acc[c][t], sa, sb[t]);
+        for (int t = 0; t < 4; ++t) acc[j][t] = PF_MFMA(A[j], B[t], acc[j][t], sa[j], sb[t]);
       }
     }
   }
@@ -178,18 +240,17 @@ __global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
   // epilogue: lanes < 32 hold routes 8 chunk + 4 g + q (hi + lo rows summed) at output column i of each tile
   if constexpr (GATEUP) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c >= nch) continue;
-      const int chunk = 4 * rh + c;
-      float gv[2][4], uv[2][4];
+    for (int j = 0; j < NJ; ++j) {
+      if (!(live & (1u << j))) continue;
+      const int chunk = cb + Sh::CSTEP * j;
+      float uv[2][4];
       uint16_t gt[2][4];
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          gv[b][q] = acc[c][b][q] + __shfl_xor(acc[c][b][q], 32, 64);
-          uv[b][q] = acc[c][2 + b][q] + __shfl_xor(acc[c][2 + b][q], 32, 64);
-          gt[b][q] = f32_to_bf16(gv[b][q]);
+          gt[b][q] = f32_to_bf16(acc[j][b][q] + __shfl_xor(acc[j][b][q], 32, 64));
+          uv[b][q] = acc[j][2 + b][q] + __shfl_xor(acc[j][2 + b][q], 32, 64);
         }
       float sg[2][4];
 #pragma unroll
@@ -225,7 +286,7 @@ __global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
         const int r = 8 * chunk + 4 * g + q;
         if (lane < 32 && r < nvalid) {
           const size_t p = (size_t)(beg + r);
-          const int n = n0 + 32 * ng;
+          const int n = n0 + 32 * tg;
           a.hq_hi[p * a.I + n + i] = (uint8_t)hc[0];
           a.hq_hi[p * a.I + n + 16 + i] = (uint8_t)hc[1];
           a.hq_lo[p * a.I + n + i] = (uint8_t)lc[0];
@@ -239,18 +300,50 @@ __global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c >= nch) continue;
-      const int chunk = 4 * rh + c;
+    for (int j = 0; j < NJ; ++j) {
+      if (!(live & (1u << j))) continue;
+      const int chunk = cb + Sh::CSTEP * j;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float v = acc[c][t][q] + __shfl_xor(acc[c][t][q], 32, 64);
+          const float v = acc[j][t][q] + __shfl_xor(acc[j][t][q], 32, 64);
           const int r = 8 * chunk + 4 * g + q;
-          if (lane < 32 && r < nvalid) a.Y[(size_t)(beg + r) * a.H + n0 + 64 * ng + 16 * t + i] = f32_to_bf16(v);
+          if (lane < 32 && r < nvalid) a.Y[(size_t)(beg + r) * a.H + n0 + 64 * tg + 16 * t + i] = f32_to_bf16(v);
         }
     }
+  }
+}
+
+// One launch covers both tile shapes.  Workgroups go to the 8 XCDs round robin (hardware block b runs on XCD
+// b % 8); XCD x takes the x-th eighth of the wide (tile, output block) list and of the narrow one, output blocks
+// fastest, interleaved in proportion so MFMA-bound wide blocks and HBM-bound narrow blocks run side by side.
+// The 1-D grid has at least 8 ceil(used / 8) blocks per list; the rest exit at once.
+template <bool GATEUP>
+__global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
+  extern __shared__ __align__(256) uint8_t pl[];
+  __shared__ int s_tok[PF_WIDE_ROWS];
+  const int4 hdr = a.tiles[0];                   // (wide tiles, narrow tiles)
+  const int obW = GATEUP ? a.I / 128 : a.H / 256;
+  const int obS = GATEUP ? a.I / 256 : a.H / 512;
+  const int usedW = __builtin_amdgcn_readfirstlane(hdr.x) * obW;
+  const int usedS = __builtin_amdgcn_readfirstlane(hdr.y) * obS;
+  const int perW = (usedW + 7) / 8, perS = (usedS + 7) / 8;
+  const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int nWx = max(0, min(perW, usedW - x * perW)), nSx = max(0, min(perS, usedS - x * perS));
+  const int n = nWx + nSx;
+  if (j >= n) return;
+  const int wb = (int)(((long long)j * nWx) / n);           // wide blocks before position j
+  if ((int)(((long long)(j + 1) * nWx) / n) > wb) {
+    const int l = x * perW + wb, tile = l / obW;
+    const int4 tt = a.tiles[1 + tile];
+    pf_tile<GATEUP, true>(a, pl, s_tok, __builtin_amdgcn_readfirstlane(tt.x), __builtin_amdgcn_readfirstlane(tt.y),
+                          __builtin_amdgcn_readfirstlane(tt.z - tt.y), l - tile * obW);
+  } else {
+    const int l = x * perS + (j - wb), tile = l / obS;
+    const int4 tt = a.tiles[1 + a.wcap + tile];
+    pf_tile<GATEUP, false>(a, pl, s_tok, __builtin_amdgcn_readfirstlane(tt.x), __builtin_amdgcn_readfirstlane(tt.y),
+                           __builtin_amdgcn_readfirstlane(tt.z - tt.y), l - tile * obS);
   }
 }
 
@@ -284,7 +377,7 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(const uint16_t* __
 
 // ------------------------------------------------------------------ host
 struct PrefillWs {
-  int32_t *hist, *perm, *inv, *offsets, *tile_off, *status, *slot_inds;
+  int32_t *hist, *perm, *inv, *offsets, *status, *slot_inds;
   int4* tiles;
   float *logits, *w;
   int32_t* inds;
@@ -293,16 +386,30 @@ struct PrefillWs {
   uint16_t* Y;
 };
 
+// Tile capacities: a wide tile holds more than narrow_max routes (or, with narrow tiles off, at least one), so
+// sum_s ceil(count_s / 96) <= P / 96 + #{s : count_s > narrow_max}; at most one narrow tile per slot.
+struct PfTiling {
+  int narrow_max, wcap, scap;
+};
+static PfTiling pf_tiling(int64_t P, int S, int H, int I) {
+  PfTiling t;
+  const bool narrow = I % 256 == 0 && H % 512 == 0;    // a narrow block's 512 weight rows must divide the outputs
+  t.narrow_max = narrow ? PF_NARROW_MAX : 0;
+  t.wcap = (int)(P / PF_WIDE_ROWS + std::min<int64_t>(S, P / (t.narrow_max + 1)) + 1);
+  t.scap = narrow ? (int)std::min<int64_t>(S, P) : 0;
+  return t;
+}
+
 static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int E) {
   PrefillWs w{};
   const size_t P = (size_t)T * k;
+  const PfTiling tl = pf_tiling((int64_t)P, S, H, I);
   w.status = c.take<int32_t>(1);
   w.hist = reinterpret_cast<int32_t*>(c.take<char>(dispatch_workspace((int)P, S)));
   w.perm = c.take<int32_t>(P);
   w.inv = c.take<int32_t>(P);
   w.offsets = c.take<int32_t>(S + 1);
-  w.tile_off = c.take<int32_t>(S + 1);
-  w.tiles = c.take<int4>(P / PF_ROWS + S + 1);      // bound on sum_s ceil(count_s / PF_ROWS), plus one
+  w.tiles = c.take<int4>(1 + (size_t)tl.wcap + tl.scap);
   if (E > 0) {
     w.logits = c.take<float>((size_t)T * E);
     w.inds = c.take<int32_t>(P);
@@ -333,21 +440,21 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   int err;
   const uint16_t* sig = sigtab_device(&err);
   if (!sig) return err;
-  int rc = launch_dispatch(slot_inds, P, S, ws.hist, ws.perm, ws.offsets, ws.inv, PF_ROWS, ws.tile_off, ws.tiles,
-                           ws.status, st);
+  const PfTiling tl = pf_tiling(P, S, H, I);
+  const TileSpec spec{tl.narrow_max, PF_WIDE_ROWS, tl.wcap};
+  int rc = launch_dispatch(slot_inds, P, S, ws.hist, ws.perm, ws.offsets, ws.inv, &spec, ws.tiles, ws.status, st);
   if (rc) return rc;
   rc = launch_quantize_fp8_hilo(x, T, H, ws.xq_hi, ws.xq_hs, ws.xq_lo, ws.xq_ls, st);
   if (rc) return rc;
   PrefillArgs a{};
   a.xq_hi = ws.xq_hi; a.xq_lo = ws.xq_lo; a.xq_hs = ws.xq_hs; a.xq_ls = ws.xq_ls;
-  a.perm = ws.perm; a.offsets = ws.offsets; a.tile_off = ws.tile_off; a.inv = ws.inv; a.w = wts; a.tiles = ws.tiles;
+  a.perm = ws.perm; a.offsets = ws.offsets; a.inv = ws.inv; a.w = wts; a.tiles = ws.tiles; a.wcap = tl.wcap;
   a.T = T; a.k = k; a.S = S; a.H = H; a.I = I; a.P = P;
   a.gate_w = bank->gate_w; a.up_w = bank->up_w; a.down_w = bank->down_w;
   a.gate_s = bank->gate_s; a.up_s = bank->up_s; a.down_s = bank->down_s;
   a.sigtab = sig;
   a.hq_hi = ws.hq_hi; a.hq_lo = ws.hq_lo; a.hq_hs = ws.hq_hs; a.hq_ls = ws.hq_ls;
   a.Y = ws.Y; a.y = y;
-  const int max_tiles = P / PF_ROWS + S;     // bound on sum_s ceil(count_s / PF_ROWS)
   static int allowed_gu = 0, allowed_dn = 0;
   if (!allowed_gu) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<true>),
@@ -361,10 +468,13 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
     if (e != hipSuccess) return set_error(MIMO_ERR_HIP, "prefill LDS attribute: %s", hipGetErrorString(e));
     allowed_dn = 1;
   }
-  // 1-D grids: 8 x ceil(bound / 8) blocks, so every XCD has an index for each of its (tile, output block)
-  // pairs; blocks past the used pairs exit at once
-  const int grid_gu = 8 * ((max_tiles * (I / 128) + 7) / 8);
-  const int grid_dn = 8 * ((max_tiles * (H / 256) + 7) / 8);
+  // 1-D grids: 8 x (ceil(wide bound / 8) + ceil(narrow bound / 8)) blocks, so every XCD has an index for each
+  // of its (tile, output block) pairs; blocks past the used pairs exit at once
+  auto grid_of = [&](int obW, int obS) {
+    return 8 * (int)(((int64_t)tl.wcap * obW + 7) / 8 + ((int64_t)tl.scap * obS + 7) / 8);
+  };
+  const int grid_gu = grid_of(I / 128, I / 256);
+  const int grid_dn = grid_of(H / 256, H / 512);
   { ProfScope p(st, "prefill_gateup"); prefill_gemm_kernel<true><<<grid_gu, 512, PF_LDS, st>>>(a); }
   { ProfScope p(st, "prefill_down"); prefill_gemm_kernel<false><<<grid_dn, 512, PF_LDS, st>>>(a); }
   { ProfScope p(st, "prefill_combine");

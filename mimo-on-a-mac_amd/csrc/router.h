@@ -39,8 +39,14 @@ int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int
 int launch_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling, int32_t* inds,
                          float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
                          hipStream_t st);
+// Row tiles of the grouped GEMM: a slot with 1..narrow_max routes is one narrow tile; a larger one is split into
+// ceil(count / wide_rows) wide tiles of near-equal whole 8-route chunks.  tiles[0] = (wide count, narrow count),
+// wide tile t at tiles[1 + t], narrow tile t at tiles[1 + wcap + t], each (slot, first route, end route, 0).
+struct TileSpec {
+  int narrow_max, wide_rows, wcap;
+};
 int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
-                    int32_t* inv, int tile_rows, int32_t* tile_off, int4* tiles, int32_t* status, hipStream_t st);
+                    int32_t* inv, const TileSpec* spec, int4* tiles, int32_t* status, hipStream_t st);
 size_t dispatch_workspace(int n, int n_slots);
 int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint8_t* hi, uint8_t* hs, uint8_t* lo,
                              uint8_t* ls, hipStream_t st);

@@ -307,52 +307,58 @@ __global__ void __launch_bounds__(1024) dispatch_hist_kernel(const int32_t* __re
   for (int s = threadIdx.x; s < n_slots; s += blockDim.x) hist[(size_t)blockIdx.x * n_slots + s] = h[s];
 }
 
-// offsets[s] = exclusive scan of per-slot totals; base[b][s] = offsets[s] + sum_{b' < b} hist[b'][s];
-// tile_off[s] = exclusive scan of ceil(count[s] / tile_rows) (row tiles of the grouped GEMM); tiles[t] =
-// (slot, first sorted route, end route, 0) of row tile t.
+// offsets[s] = exclusive scan of per-slot totals; base[b][s] = offsets[s] + sum_{b' < b} hist[b'][s]; with a
+// TileSpec, the row tiles of each slot (see TileSpec).  One thread per slot (n_slots <= 1024), wave scans.
 __global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int n_slots,
-                                                             int32_t* __restrict__ offsets, int tile_rows,
-                                                             int32_t* __restrict__ tile_off, int4* __restrict__ tiles) {
-  extern __shared__ int sh[];
-  int* tot = sh;
-  int* til = sh + n_slots;
-  for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
-    int acc = 0;
-    for (int b = 0; b < nchunks; ++b) acc += hist[(size_t)b * n_slots + s];
-    tot[s] = acc;
-    til[s] = tile_rows > 0 ? (acc + tile_rows - 1) / tile_rows : 0;
+                                                             int32_t* __restrict__ offsets, TileSpec spec,
+                                                             int4* __restrict__ tiles) {
+  __shared__ int wsum[3][16];
+  const int s = threadIdx.x, lane = s & 63, wv = s >> 6;
+  int c = 0;
+  if (s < n_slots)
+    for (int b = 0; b < nchunks; ++b) c += hist[(size_t)b * n_slots + s];
+  const int nw = (tiles && c > spec.narrow_max) ? (c + spec.wide_rows - 1) / spec.wide_rows : 0;
+  const int ns = (tiles && c >= 1 && c <= spec.narrow_max) ? 1 : 0;
+  int v0 = c, v1 = nw, v2 = ns;                  // inclusive scans within the wave
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u0 = __shfl_up(v0, d, 64), u1 = __shfl_up(v1, d, 64), u2 = __shfl_up(v2, d, 64);
+    if (lane >= d) {
+      v0 += u0;
+      v1 += u1;
+      v2 += u2;
+    }
+  }
+  if (lane == 63) {
+    wsum[0][wv] = v0;
+    wsum[1][wv] = v1;
+    wsum[2][wv] = v2;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0, trun = 0;
-    for (int s = 0; s < n_slots; ++s) {
-      int c = tot[s], tc = til[s];
-      tot[s] = run;
-      til[s] = trun;
-      run += c;
-      trun += tc;
-    }
-    offsets[n_slots] = run;
-    if (tile_off) tile_off[n_slots] = trun;
+  for (int w = 0; w < wv; ++w) {
+    v0 += wsum[0][w];
+    v1 += wsum[1][w];
+    v2 += wsum[2][w];
   }
-  __syncthreads();
-  for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
-    offsets[s] = tot[s];
-    if (tile_off) tile_off[s] = til[s];
-    if (tiles) {
-      const int end = s + 1 < n_slots ? tot[s + 1] : offsets[n_slots];
-      const int t1 = s + 1 < n_slots ? til[s + 1] : tile_off[n_slots];
-      for (int t = til[s]; t < t1; ++t) {
-        const int b = tot[s] + (t - til[s]) * tile_rows;
-        tiles[t] = make_int4(s, b, b + tile_rows < end ? b + tile_rows : end, 0);
-      }
+  if (s >= n_slots) return;
+  const int e0 = v0 - c, e1 = v1 - nw, e2 = v2 - ns;   // exclusive prefixes
+  offsets[s] = e0;
+  if (s == n_slots - 1) {
+    offsets[n_slots] = v0;
+    if (tiles) tiles[0] = make_int4(v1, v2, 0, 0);
+  }
+  if (nw) {
+    const int chunks = (c + 7) / 8;
+    for (int q = 0; q < nw; ++q) {
+      const int c0 = (int)((int64_t)q * chunks / nw), c1 = (int)((int64_t)(q + 1) * chunks / nw);
+      tiles[1 + e1 + q] = make_int4(s, e0 + 8 * c0, e0 + min(8 * c1, c), 0);
     }
-    int acc = tot[s];
-    for (int b = 0; b < nchunks; ++b) {
-      int c = hist[(size_t)b * n_slots + s];
-      hist[(size_t)b * n_slots + s] = acc;
-      acc += c;
-    }
+  }
+  if (ns) tiles[1 + spec.wcap + e2] = make_int4(s, e0, e0 + c, 0);
+  int acc = e0;
+  for (int b = 0; b < nchunks; ++b) {
+    const int h = hist[(size_t)b * n_slots + s];
+    hist[(size_t)b * n_slots + s] = acc;
+    acc += h;
   }
 }
 
@@ -385,13 +391,14 @@ __global__ void __launch_bounds__(1024) dispatch_place_kernel(const int32_t* __r
 }
 
 int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
-                    int32_t* inv, int tile_rows, int32_t* tile_off, int4* tiles, int32_t* status, hipStream_t st) {
+                    int32_t* inv, const TileSpec* spec, int4* tiles, int32_t* status, hipStream_t st) {
   int nchunks = (n + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK;
   if (nchunks == 0) nchunks = 1;
   ProfScope p(st, "prefill_dispatch");
   dispatch_hist_kernel<<<nchunks, 1024, n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, status);
-  dispatch_scan_kernel<<<1, 1024, 2 * n_slots * sizeof(int), st>>>(hist, nchunks, n_slots, offsets, tile_rows,
-                                                                     tile_off, tiles);
+  const TileSpec none{0, 1, 0};
+  dispatch_scan_kernel<<<1, 1024, 0, st>>>(hist, nchunks, n_slots, offsets, spec ? *spec : none,
+                                            spec ? tiles : nullptr);
   if (n > 0)
     dispatch_place_kernel<<<nchunks, 1024, 16 * n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, perm, inv);
   return check_launch("prefill dispatch");
@@ -485,7 +492,7 @@ int mimo_prefill_dispatch(const int32_t* slot_inds, int T, int k, int n_slots, i
                "prefill_dispatch: need 1 <= n_slots <= 1024");
   MIMO_REQUIRE(ws && ws_bytes >= dispatch_workspace(T * k, n_slots), MIMO_ERR_WORKSPACE,
                "prefill_dispatch: workspace too small");
-  return launch_dispatch(slot_inds, T * k, n_slots, static_cast<int32_t*>(ws), perm, offsets, inv, 0, nullptr, nullptr,
+  return launch_dispatch(slot_inds, T * k, n_slots, static_cast<int32_t*>(ws), perm, offsets, inv, nullptr, nullptr,
                          nullptr, as_stream(stream));
 }
 
