@@ -34,17 +34,20 @@ struct PrefillArgs {
 };
 
 // Row tiles.  The dispatch cuts each slot's sorted routes into tiles of one of two shapes:
-//   narrow: a slot with at most 32 routes (4 chunks of 8) is one tile, multiplied by 512 weight rows per block
+//   narrow: a slot with at most 32 routes (2 chunks of 16) is one tile, multiplied by 512 weight rows per block
 //           (gate/up: 256 outputs of each projection; down: 512 outputs).  These blocks stream weights at the
 //           HBM rate with little MFMA work, so the wider weight tile halves their activation re-reads.
-//   wide:   a larger slot is split into ceil(count / 96) tiles of near-equal whole 8-route chunks (at most 12),
+//   wide:   a larger slot is split into ceil(count / 96) tiles of near-equal whole 16-route chunks (at most 6),
 //           multiplied by 256 weight rows per block (128 + 128 outputs, or 256 down outputs).
+// An MFMA multiplies 16 routes of one activation plane by 16 weight rows; the hi and lo planes accumulate into
+// the same tile, so each accumulator lane holds finished sums for 4 routes.
 // Both shapes stage 40 KB per K-step of 128 through a 3-slot LDS ring: the hi and lo activation code planes of
 // the tile's routes and the block's E2M1 weight rows.  The E8M0 scales of 8 K-steps (32 bytes per row) are
 // copied at once into one of two epoch buffers, one 4-byte word per lane, so scale traffic costs one request
 // per row every 8 steps.
 constexpr int PF_NARROW_MAX = 32;
 constexpr int PF_WIDE_ROWS = 96;
+constexpr int PF_UNIT = 16;                          // routes per MFMA chunk
 constexpr int PF_STAGES = 3;                         // one step multiplied while two are in flight
 constexpr int PF_STAGE = 41216;
 constexpr int PF_EPOCH = 8;                          // K-steps per scale copy
@@ -55,16 +58,18 @@ constexpr int PF_LDS = PF_SC + 2 * PF_SC_BYTES;      // 160512 bytes
 // Stage layout: A planes of R routes x 128 codes, the 16-byte chunk q of route r at slot q ^ (r & 7), the lo
 // plane 128 bytes off the hi plane's bank phase; B rows of 64 bytes, chunk g of row r at slot (g + (r & 15) / 4)
 // & 3.  Both make the MFMA operand reads conflict-free.  Copies per wave: ACOP + BCOP per K-step (5 in both
-// shapes), ECOP per epoch.  A wave multiplies 4 weight tiles (64 rows) by NJ chunks spaced CSTEP apart.
+// shapes, one per 8-route block of a plane or 16 weight rows), ECOP per epoch.  A wave multiplies 4 weight
+// tiles (64 rows) by NJ 16-route chunks spaced CSTEP apart.
 template <bool WIDE> struct PfShape;
 template <> struct PfShape<false> {
-  static constexpr int R = 32, NCH = 4, N = 512, A_PL = 4224, B_OFF = 8448;
-  static constexpr int ACOP = 1, BCOP = 4, ECOP = 9, NJ = 4, CSTEP = 1;
+  static constexpr int R = 32, CB = 4, N = 512, A_PL = 4224, B_OFF = 8448;
+  static constexpr int ACOP = 1, BCOP = 4, ECOP = 9, NJ = 2, CSTEP = 1;
 };
 template <> struct PfShape<true> {
-  static constexpr int R = 96, NCH = 12, N = 256, A_PL = 12416, B_OFF = 24832;
-  static constexpr int ACOP = 3, BCOP = 2, ECOP = 7, NJ = 6, CSTEP = 2;
+  static constexpr int R = 96, CB = 12, N = 256, A_PL = 12416, B_OFF = 24832;
+  static constexpr int ACOP = 3, BCOP = 2, ECOP = 7, NJ = 3, CSTEP = 2;
 };
+constexpr int PF_STG = 6144;                         // per-wave output staging after the K loop
 
 // s_waitcnt vmcnt(n) for the counts of the K loop (0, 5, 5 + 7, 5 + 9); a smaller count only waits longer
 __device__ __forceinline__ void pf_wait(int n) {
@@ -114,11 +119,11 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 #pragma unroll
   for (int c = 0; c < Sh::ACOP; ++c) {
     const int b = Sh::ACOP * wave + c;
-    const int r = 8 * (b % Sh::NCH) + (lane >> 3);
+    const int r = 8 * (b % Sh::CB) + (lane >> 3);
     a_off[c] = r < nvalid ? (uint32_t)s_tok[r] * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (r & 7))
                           : (uint32_t)s_tok[0] * (uint32_t)K;
-    a_src[c] = b >= Sh::NCH ? a_lo : a_hi;
-    a_dst[c] = (b >= Sh::NCH ? Sh::A_PL : 0) + 1024 * (b % Sh::NCH);
+    a_src[c] = b >= Sh::CB ? a_lo : a_hi;
+    a_dst[c] = (b >= Sh::CB ? Sh::A_PL : 0) + 1024 * (b % Sh::CB);
   }
   // B copies: block rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding chunk (slot - row / 4) & 3
   const bool up_half = GATEUP && wave >= 4;
@@ -170,12 +175,12 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   };
 
   // the wave's tiles: weight rows 64 tg .. (GATEUP t = 2 p + b: projection p, 16-output half b), chunks
-  // cb + CSTEP j for j < nj
+  // cb + CSTEP j (routes 16 chunk ..) for the live j
   const int tg = WIDE ? (wave & 3) : wave;
   const int cb = WIDE ? (wave >> 2) : 0;
-  uint32_t live = 0;                             // bit j: chunk cb + CSTEP j holds routes
+  uint32_t live = 0;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) live |= (8 * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
+  for (int j = 0; j < NJ; ++j) live |= (PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
   live = __builtin_amdgcn_readfirstlane(live);
   int brow[4], bsc[4], bsw[4];
 #pragma unroll
@@ -185,15 +190,19 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     bsw[t] = pf_swz<R>(2 * R + brow[t]);
   }
   const int bslot = 16 * ((g + (i >> 2)) & 3);
-  int aoff[NJ], asc[NJ], asw[NJ];
+  // A operand of chunk j, plane p: route row r = 16 chunk + i, chunks g and 4 + g of its 128 codes
+  int aoff[NJ], asc[NJ][2], asw[NJ][2];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int r = 8 * (cb + Sh::CSTEP * j) + (i & 7);
-    const int q = (i >> 3) * R + r;
-    aoff[j] = (i >> 3) * Sh::A_PL + 128 * r;
-    asc[j] = 32 * q + g;
-    asw[j] = pf_swz<R>(q);
+    const int r = PF_UNIT * (cb + Sh::CSTEP * j) + i;
+    aoff[j] = 128 * r;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      asc[j][p] = 32 * (p * R + r) + g;
+      asw[j][p] = pf_swz<R>(p * R + r);
+    }
   }
+  const int sw_lo = 16 * (g ^ (i & 7)), sw_hi = 16 * ((4 + g) ^ (i & 7));
   v4f acc[NJ][4];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -218,52 +227,60 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
       B[t] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
       sb[t] = sc[bsc[t] + 4 * (kw ^ bsw[t])];
     }
-    v8i A[NJ];
-    int sa[NJ];
+    v8i A[NJ][2];
+    int sa[NJ][2];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {              // read unconditionally: fixed LDS counts let each MFMA group
-      const uint8_t* ab = st + aoff[j];         // wait for its own operands only
-      const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + 16 * (g ^ (i & 7)));
-      const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + 16 * ((4 + g) ^ (i & 7)));
-      A[j] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
-      sa[j] = sc[asc[j] + 4 * (kw ^ asw[j])];
-    }
+    for (int j = 0; j < NJ; ++j)                 // read unconditionally: fixed LDS counts let each MFMA group
+#pragma unroll                                   // wait for its own operands only
+      for (int p = 0; p < 2; ++p) {
+        const uint8_t* ab = st + p * Sh::A_PL + aoff[j];
+        const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + sw_lo);
+        const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + sw_hi);
+        A[j][p] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
+        sa[j][p] = sc[asc[j][p] + 4 * (kw ^ asw[j][p])];
+      }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (live & (1u << j)) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[j][t] = PF_MFMA(A[j], B[t], acc[j][t], sa[j], sb[t]);
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[j][t] = PF_MFMA(A[j][p], B[t], acc[j][t], sa[j][p], sb[t]);
       }
     }
   }
 
-  // epilogue: lanes < 32 hold routes 8 chunk + 4 g + q (hi + lo rows summed) at output column i of each tile
+  // epilogue: lane (i, g) holds routes 16 chunk + 4 g + q at output column i of each tile.  Results go through
+  // a per-wave LDS staging area (the ring is free once every wave has left the K loop) so that the global
+  // stores are 16 bytes per lane.
+  __syncthreads();
+  uint8_t* stg = pl + PF_STG * wave;
   if constexpr (GATEUP) {
+    // staging: [16 NJ routes][hi 32 bytes | lo 32 bytes], then the routes' (hi, lo) scale bytes
+    uint8_t* ssc = stg + 64 * PF_UNIT * NJ;
+    uint16_t gt[NJ][2][4], sgv[NJ][2][4];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) gt[j][b][q] = f32_to_bf16(acc[j][b][q]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)                 // every sigmoid lookup in flight before the first use
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sgv[j][b][q] = a.sigtab[gt[j][b][q]];   // any 16-bit index is in the table
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (!(live & (1u << j))) continue;
-      const int chunk = cb + Sh::CSTEP * j;
-      float uv[2][4];
-      uint16_t gt[2][4];
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          gt[b][q] = f32_to_bf16(acc[j][b][q] + __shfl_xor(acc[j][b][q], 32, 64));
-          uv[b][q] = acc[j][2 + b][q] + __shfl_xor(acc[j][2 + b][q], 32, 64);
-        }
-      float sg[2][4];
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sg[b][q] = bf16_to_f32(a.sigtab[gt[b][q]]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float hv[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-          const float gtf = bf16_to_f32(gt[b][q]);
-          hv[b] = round_bf16(round_bf16(gtf * sg[b][q]) * round_bf16(uv[b][q]));
+          const float gtf = bf16_to_f32(gt[j][b][q]);
+          hv[b] = round_bf16(round_bf16(gtf * bf16_to_f32(sgv[j][b][q])) * round_bf16(acc[j][2 + b][q]));
         }
         // the wave's 32 outputs of this route are one E8M0 block of h: max over b and the 16 lanes of the row
         const float am = dpp_group_max16(fmaxf(fabsf(hv[0]), fabsf(hv[1])));
@@ -283,34 +300,53 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
           float dec;
           lc[b] = e4m3_encode(res[b], Yx, &dec);
         }
-        const int r = 8 * chunk + 4 * g + q;
-        if (lane < 32 && r < nvalid) {
-          const size_t p = (size_t)(beg + r);
-          const int n = n0 + 32 * tg;
-          a.hq_hi[p * a.I + n + i] = (uint8_t)hc[0];
-          a.hq_hi[p * a.I + n + 16 + i] = (uint8_t)hc[1];
-          a.hq_lo[p * a.I + n + i] = (uint8_t)lc[0];
-          a.hq_lo[p * a.I + n + 16 + i] = (uint8_t)lc[1];
-          if (i == 0) {
-            a.hq_hs[p * (a.I / 32) + n / 32] = (uint8_t)(X + 127);
-            a.hq_ls[p * (a.I / 32) + n / 32] = (uint8_t)(Yx + 127);
-          }
+        const int rl = PF_UNIT * j + 4 * g + q;  // route of the wave's staging
+        uint8_t* row = stg + 64 * rl;
+        row[i] = (uint8_t)hc[0];
+        row[16 + i] = (uint8_t)hc[1];
+        row[32 + i] = (uint8_t)lc[0];
+        row[48 + i] = (uint8_t)lc[1];
+        if (i == 0) {
+          ssc[2 * rl] = (uint8_t)(X + 127);
+          ssc[2 * rl + 1] = (uint8_t)(Yx + 127);
+        }
+      }
+    }
+    const int n = n0 + 32 * tg;                  // the wave's 32 outputs
+#pragma unroll
+    for (int k = 0; k < NJ; ++k) {               // 16 routes x 4 pieces of 16 bytes per pass
+      const int rl = PF_UNIT * k + (lane >> 2), part = lane & 3;
+      const int r = PF_UNIT * (cb + Sh::CSTEP * k) + (lane >> 2);
+      if ((live & (1u << k)) && r < nvalid) {
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + 64 * rl + 16 * part);
+        uint8_t* dst = (part >> 1) ? a.hq_lo : a.hq_hi;
+        *reinterpret_cast<uint4*>(dst + (size_t)(beg + r) * a.I + n + 16 * (part & 1)) = v;
+        if (part == 0) {
+          a.hq_hs[(size_t)(beg + r) * (a.I / 32) + n / 32] = ssc[2 * rl];
+          a.hq_ls[(size_t)(beg + r) * (a.I / 32) + n / 32] = ssc[2 * rl + 1];
         }
       }
     }
   } else {
+    // staging: [16 NJ routes][64 outputs] bf16
+    uint16_t* stg16 = reinterpret_cast<uint16_t*>(stg);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (!(live & (1u << j))) continue;
-      const int chunk = cb + Sh::CSTEP * j;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float v = acc[j][t][q] + __shfl_xor(acc[j][t][q], 32, 64);
-          const int r = 8 * chunk + 4 * g + q;
-          if (lane < 32 && r < nvalid) a.Y[(size_t)(beg + r) * a.H + n0 + 64 * tg + 16 * t + i] = f32_to_bf16(v);
-        }
+        for (int q = 0; q < 4; ++q) stg16[64 * (PF_UNIT * j + 4 * g + q) + 16 * t + i] = f32_to_bf16(acc[j][t][q]);
+    }
+#pragma unroll
+    for (int k = 0; k < 2 * NJ; ++k) {           // 8 routes x 8 pieces of 16 bytes per pass
+      const int rl = 8 * k + (lane >> 3), part = lane & 7;
+      const int j = rl >> 4;
+      const int r = PF_UNIT * (cb + Sh::CSTEP * j) + (rl & 15);
+      if ((live & (1u << j)) && r < nvalid) {
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + 128 * rl + 16 * part);
+        *reinterpret_cast<uint4*>(a.Y + (size_t)(beg + r) * a.H + n0 + 64 * tg + 8 * part) = v;
+      }
     }
   }
 }
@@ -441,7 +477,7 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   const uint16_t* sig = sigtab_device(&err);
   if (!sig) return err;
   const PfTiling tl = pf_tiling(P, S, H, I);
-  const TileSpec spec{tl.narrow_max, PF_WIDE_ROWS, tl.wcap};
+  const TileSpec spec{tl.narrow_max, PF_WIDE_ROWS, tl.wcap, PF_UNIT};
   int rc = launch_dispatch(slot_inds, P, S, ws.hist, ws.perm, ws.offsets, ws.inv, &spec, ws.tiles, ws.status, st);
   if (rc) return rc;
   rc = launch_quantize_fp8_hilo(x, T, H, ws.xq_hi, ws.xq_hs, ws.xq_lo, ws.xq_ls, st);

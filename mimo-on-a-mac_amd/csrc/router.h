@@ -40,10 +40,11 @@ int launch_router_select(const float* logits, const float* bias, int T, int E, i
                          float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
                          hipStream_t st);
 // Row tiles of the grouped GEMM: a slot with 1..narrow_max routes is one narrow tile; a larger one is split into
-// ceil(count / wide_rows) wide tiles of near-equal whole 8-route chunks.  tiles[0] = (wide count, narrow count),
-// wide tile t at tiles[1 + t], narrow tile t at tiles[1 + wcap + t], each (slot, first route, end route, 0).
+// ceil(count / wide_rows) wide tiles of near-equal whole unit-route chunks (wide_rows a multiple of unit).
+// tiles[0] = (wide count, narrow count), wide tile t at tiles[1 + t], narrow tile t at tiles[1 + wcap + t], each
+// (slot, first route, end route, 0).
 struct TileSpec {
-  int narrow_max, wide_rows, wcap;
+  int narrow_max, wide_rows, wcap, unit;
 };
 int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int32_t* perm, int32_t* offsets,
                     int32_t* inv, const TileSpec* spec, int4* tiles, int32_t* status, hipStream_t st);

@@ -347,10 +347,10 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict
     if (tiles) tiles[0] = make_int4(v1, v2, 0, 0);
   }
   if (nw) {
-    const int chunks = (c + 7) / 8;
+    const int chunks = (c + spec.unit - 1) / spec.unit;
     for (int q = 0; q < nw; ++q) {
       const int c0 = (int)((int64_t)q * chunks / nw), c1 = (int)((int64_t)(q + 1) * chunks / nw);
-      tiles[1 + e1 + q] = make_int4(s, e0 + 8 * c0, e0 + min(8 * c1, c), 0);
+      tiles[1 + e1 + q] = make_int4(s, e0 + spec.unit * c0, e0 + min(spec.unit * c1, c), 0);
     }
   }
   if (ns) tiles[1 + spec.wcap + e2] = make_int4(s, e0, e0 + c, 0);
@@ -396,7 +396,7 @@ int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int
   if (nchunks == 0) nchunks = 1;
   ProfScope p(st, "prefill_dispatch");
   dispatch_hist_kernel<<<nchunks, 1024, n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, status);
-  const TileSpec none{0, 1, 0};
+  const TileSpec none{0, 1, 0, 1};
   dispatch_scan_kernel<<<1, 1024, 0, st>>>(hist, nchunks, n_slots, offsets, spec ? *spec : none,
                                             spec ? tiles : nullptr);
   if (n > 0)
