@@ -6,6 +6,7 @@
 namespace mimo {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ bf16
@@ -254,19 +255,28 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
 }
+// The base address operands of these copies are SGPRs that are often written by v_readfirstlane just before
+// the asm; a VMEM instruction reading an SGPR that a VALU instruction wrote needs 5 wait states, which the
+// compiler does not supply inside inline assembly: each asm starts with them (s_nop 4 = 5 wait states).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"     // M0 is declared clobbered on purpose
 __device__ __forceinline__ void lds_copy16(const void* gbase, uint32_t voff, const void* lds_dst) {
   const uint64_t b = uniform_u64((uint64_t)gbase);
   const uint32_t m = lds_addr(lds_dst);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(m)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(b), "s"(m)
                : "memory", "m0");
 }
 __device__ __forceinline__ void lds_copy4(const void* gbase, uint32_t voff, const void* lds_dst) {
   const uint64_t b = uniform_u64((uint64_t)gbase);
   const uint32_t m = lds_addr(lds_dst);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(b), "s"(m)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(b), "s"(m)
                : "memory", "m0");
+}
+// 16 bytes per lane global -> VGPRs, not tracked by the compiler's wait counting: the caller waits for it with
+// an explicit s_waitcnt before any use (and pins the use below that wait)
+__device__ __forceinline__ void gload16(v4i& dst, const void* gbase, uint32_t voff) {
+  const uint64_t b = uniform_u64((uint64_t)gbase);
+  asm volatile("s_nop 4\n\tglobal_load_dwordx4 %0, %1, %2" : "=v"(dst) : "v"(voff), "s"(b) : "memory");
 }
 #pragma clang diagnostic pop
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every global load of the wave has landed,
