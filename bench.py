@@ -53,10 +53,16 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-run", action="store_true",
-                    help="profiling payload: a 1 GiB calibration copy, then 1-row decode steps over 8 layers")
+                    help="profiling payload: a 1 GiB calibration copy, 1-row decode steps over 8 layers, then "
+                         "2048-token prefill layers")
     ap.add_argument("--traffic-parse", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="reduce two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --traffic-run to "
                          "profiles/traffic.json")
+    ap.add_argument("--mfma-parse", metavar="PMC_DIR",
+                    help="summarise a rocprofv3 --pmc run of --traffic-run with SQ_INSTS_MFMA, "
+                         "SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE, using the kernel durations of a "
+                         "--kernel-trace run of the same payload (second argument)")
+    ap.add_argument("--mfma-trace", metavar="TRACE_DIR", help="kernel-trace directory for --mfma-parse")
     return ap.parse_args()
 
 
@@ -174,22 +180,33 @@ def decode_case(layers, M, steps, warmup, seed, device):
             "experts_only_GBps": U * 13369344 / (ms * 1e-3) / 1e9, "_fn": fn, "_U": U}
 
 
-def prefill_case(layers, T, steps, warmup, seed, device):
-    """Expert path of prefill (dispatch + grouped GEMMs + combine) with Zipf(1.1) routes, layers rotated."""
+def zipf_routes(T, seed, nin):
+    """`nin` routings of T tokens: top-8 distinct experts per token drawn with Zipf(1.1) popularity over a
+    seeded permutation of the 256 experts (Gumbel top-k on log p), and normalised random weights."""
     import numpy as np
-    import torch
     rng = np.random.default_rng(seed)
-    n = min(len(layers.blocks), 8)
-    nin = 4
     perm = rng.permutation(E)
     p = 1.0 / np.arange(1, E + 1) ** 1.1
     logp = np.log(p / p.sum())
-    Xs, Is, Ws, Us = [], [], [], []
+    out = []
     for _ in range(nin):
         g = rng.gumbel(size=(T, E)) + logp[None, :]
         inds = perm[np.argsort(-g, axis=1)[:, :K]].astype(np.int32)
         w = rng.random((T, K)).astype(np.float32)
         w /= w.sum(1, keepdims=True)
+        out.append((inds, w))
+    return out
+
+
+def prefill_case(layers, T, steps, warmup, seed, device, timed=True):
+    """Expert path of prefill (dispatch + grouped GEMMs + combine) with Zipf(1.1) routes, layers rotated.
+    With timed=False only the step function and the routing statistics are returned."""
+    import numpy as np
+    import torch
+    n = min(len(layers.blocks), 8)
+    nin = 4
+    Xs, Is, Ws, Us = [], [], [], []
+    for inds, w in zipf_routes(T, seed, nin):
         Xs.append(torch.randn(T, H, device=device).to(torch.bfloat16))
         Is.append(torch.from_numpy(inds).to(device))
         Ws.append(torch.from_numpy(w).to(device))
@@ -199,6 +216,8 @@ def prefill_case(layers, T, steps, warmup, seed, device):
     def fn(s):
         blocks[s % n]._moe_prefill(Xs[s % nin], Is[s % nin], Ws[s % nin])
 
+    if not timed:
+        return {"_fn": fn, "distinct_experts": float(np.mean(Us)), "inds": [i.cpu().numpy() for i in Is]}
     ms = time_graph(fn, steps, warmup)
     U = float(np.mean(Us))
     nbytes = U * 13369344 + 2 * T * H * 2
@@ -300,10 +319,14 @@ def _cpu_model():
 CALIB_BYTES = 1 << 30        # the calibration copy reads and writes this many bytes
 
 
+PF_TRAFFIC_T = 2048
+PF_TRAFFIC_STEPS = 8
+
+
 def traffic_run():
     """Workload for the counter runs: the calibration copy (an elementwise multiply by one over 1 GiB, so a
     kernel, not a DMA copy), then 24 one-row decode steps rotating over 8 resident layers (8 x 103 MB, more
-    than the 256 MB MALL holds)."""
+    than the 256 MB MALL holds), then 8 prefill layers of 2048 tokens with Zipf(1.1) routes, one per layer."""
     import numpy as np
     import torch
     src = torch.ones(CALIB_BYTES // 2, dtype=torch.bfloat16, device="cuda")
@@ -318,6 +341,10 @@ def traffic_run():
           for l in range(24)]
     for s in range(24):
         layers.blocks[s % 8](xs[s])
+    torch.cuda.synchronize()
+    r = prefill_case(layers, PF_TRAFFIC_T, 0, 0, seed=20 + PF_TRAFFIC_T, device="cuda", timed=False)
+    for s in range(PF_TRAFFIC_STEPS):
+        r["_fn"](s)
     torch.cuda.synchronize()
     log("[traffic] done")
 
@@ -367,18 +394,78 @@ def traffic_parse(fetch_dir, write_dir):
            "_detail": {"kernel": name, "dispatches": len(gf), "fetch_bytes": fetch, "write_bytes": write,
                        "algorithmic_bytes": algo, "fetch_scale": fetch_scale, "write_scale": write_scale,
                        "calibration": "elementwise multiply by one over 1 GiB: reads and writes 1 GiB"}}
+    rows = [("decode_gateup_kernel (1 row, 8 experts)", len(gf), fetch, write, algo)]
+    # prefill GEMMs of the payload: algorithmic bytes = distinct experts' weights and scales + activation codes
+    # and scales read + results written (hi/lo E4M3 h with scales, or bf16 Y)
+    import numpy as np
+    T, P = PF_TRAFFIC_T, PF_TRAFFIC_T * K
+    routes = zipf_routes(T, 20 + T, 4)
+    U = float(np.mean([len(np.unique(routes[s % 4][0])) for s in range(PF_TRAFFIC_STEPS)]))
+    split = lambda rows_, cols: 2 * rows_ * cols + 2 * rows_ * cols // 32          # hi + lo codes and scales
+    algo_pf = {True: U * GATEUP_BYTES_PER_EXPERT + split(T, H) + split(P, I),
+               False: U * (H * I // 2 + H * I // 32) + split(P, I) + P * H * 2}
+    for gate in (True, False):
+        key = lambda n, g=gate: f"prefill_gemm_kernel<{'true' if g else 'false'}>" in n
+        pname, pf_ = pick(f, key)
+        _, pw_ = pick(w, key)
+        pfetch = sum(pf_) / len(pf_) * fetch_scale
+        pwrite = sum(pw_) / len(pw_) * write_scale
+        tag = "prefill_gateup" if gate else "prefill_down"
+        out[f"prefill_gemm_kernel<{'true' if gate else 'false'}>:prefill_t{T}"] = pfetch + pwrite
+        out[f"_detail_{tag}"] = {"kernel": pname, "dispatches": len(pf_), "fetch_bytes": pfetch,
+                                 "write_bytes": pwrite, "algorithmic_bytes": algo_pf[gate],
+                                 "distinct_experts": U}
+        rows.append((f"prefill_gemm_kernel<{'true' if gate else 'false'}> ({T} tokens, {U:.1f} experts)",
+                     len(pf_), pfetch, pwrite, algo_pf[gate]))
     with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as fh:
         json.dump(out, fh, indent=1)
-    print(f"| kernel | dispatches | FETCH (MB/launch) | WRITE (MB/launch) | algorithmic (MB/launch) | fetch / algorithmic |")
+    print(f"| kernel | dispatches | FETCH (MB/launch) | WRITE (MB/launch) | algorithmic (MB/launch) | "
+          f"(fetch + write) / algorithmic |")
     print(f"|---|---|---|---|---|---|")
-    print(f"| decode_gateup_kernel (1 row, 8 experts) | {len(gf)} | {fetch / 1e6:.2f} | {write / 1e6:.3f} | "
-          f"{algo / 1e6:.2f} | {fetch / algo:.3f} |")
+    for nm, nd, fe, wr, al in rows:
+        print(f"| {nm} | {nd} | {fe / 1e6:.2f} | {wr / 1e6:.3f} | {al / 1e6:.2f} | {(fe + wr) / al:.3f} |")
     print(f"\ncalibration: FETCH_SIZE scale {fetch_scale:.4f}, WRITE_SIZE scale {write_scale:.4f} (bytes per counted "
           f"byte, from the 1 GiB elementwise copy)")
 
 
+def mfma_parse(pmc_dir, trace_dir):
+    """MFMA work of the prefill GEMMs from a --pmc run (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES,
+    GRBM_GUI_ACTIVE) and their durations from a --kernel-trace run of the same payload."""
+    import csv
+    import glob
+    cnt = {}
+    for r in _counter_rows(pmc_dir):
+        k = r["Kernel_Name"]
+        if "prefill_gemm_kernel" not in k:
+            continue
+        cnt.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    dur = {}
+    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if "prefill_gemm_kernel" in r["Kernel_Name"]:
+                    dur.setdefault(r["Kernel_Name"], []).append(
+                        (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
+    print("| kernel | dispatches | MFMA instr / launch | avg µs | MFMA TFLOP/s issued (hi + lo) | "
+          "useful TFLOP/s | busy cycles / instr | GRBM cycles / µs |")
+    print("|---|---|---|---|---|---|---|---|")
+    for k in sorted(cnt):
+        c = cnt[k]
+        n = len(c["SQ_INSTS_MFMA"])
+        inst = sum(c["SQ_INSTS_MFMA"]) / n
+        busy = sum(c["SQ_VALU_MFMA_BUSY_CYCLES"]) / n
+        grbm = sum(c["GRBM_GUI_ACTIVE"]) / n
+        d = sum(dur.get(k, [float("nan")])) / max(1, len(dur.get(k, [])))
+        issued = inst * 16 * 16 * 128 * 2 / d / 1e12
+        print(f"| {k.split('(')[0].replace('void mimo::', '')} | {n} | {inst:,.0f} | {d * 1e6:.1f} | "
+              f"{issued:.0f} | {issued / 2:.0f} | {busy / inst:.1f} | {grbm / (d * 1e6):.0f} |")
+
+
 def main():
     args = parse()
+    if args.mfma_parse:
+        mfma_parse(args.mfma_parse, args.mfma_trace)
+        return
     if args.traffic_parse:
         traffic_parse(*args.traffic_parse)
         return

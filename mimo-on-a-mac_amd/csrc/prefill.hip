@@ -4,14 +4,13 @@
 // Reference: _moe_prefill engine/mimo_stream/model.py:230-271 and _pair_outputs :221-228 (three sorted
 // gather_qmm calls, bf16 SwiGLU intermediate, bf16 expert outputs, inverse permutation, (Y.f32 * w).sum(1)).
 //
-// Tiling: a row tile is up to 64 consecutive sorted routes of one slot (the dispatch writes the tile table).
-// A block (8 waves) owns one row tile and 128 gate + 128 up outputs (gate/up) or 256 outputs (down).  The K
-// loop runs in steps of 128 through a 4-stage LDS ring filled by global_load_lds: per step 16 KB of
-// activation codes (hi and lo E4M3 planes of the 64 routes), 16 KB of E2M1 weights (256 rows x 64 B) and the
-// E8M0 scales; three steps are in flight while the fourth is multiplied.  Wave w takes route half w & 1 (four
-// 8-route chunks) and output group w >> 1 (four 16-output weight tiles): 16 MFMAs per step, chunks past the
-// tile's routes skipped.  Same operand layout as the decode kernels: the hi and lo halves of 8 routes fill
-// rows 0-7 and 8-15 of one MFMA.
+// Tiling: the dispatch cuts each slot's sorted routes into row tiles (narrow: a slot of at most 32 routes;
+// wide: up to 96 routes) and writes the tile table.  A block (8 waves) owns one row tile and one block of
+// weight rows (narrow 512, wide 256; gate/up blocks take half of their rows from each projection).  The K
+// loop runs in steps of 128 through a 3-slot LDS ring filled by global_load_lds (activation hi and lo E4M3
+// planes of the tile's routes, the block's E2M1 weight rows; E8M0 scales once per 8 steps); each wave
+// multiplies 16-route chunks by four 16-row weight tiles, the hi and lo planes accumulating into the same
+// tile.  The epilogue stages results in LDS and writes 16-byte pieces.
 #include "device.h"
 #include "host.h"
 #include "router.h"
