@@ -81,6 +81,17 @@ __device__ __forceinline__ uint32_t e4m3_encode(float v, int X, float* dec) {
   return mag | sgn;
 }
 
+// Two E4M3 codes (bits 0-7 and 8-15) of values already divided by their block scale (|y| <= 448) from the
+// hardware conversion (OCP E4M3, round to nearest even, checked against the oracle on every bf16 input), with
+// the sign of zero codes cleared: the codes e4m3_encode gives.
+__device__ __forceinline__ uint32_t e4m3_pack2(float y0, float y1) {
+  const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false) & 0xFFFFu;
+  const uint32_t t = w & 0x7F7Fu;
+  return t | (w & ((t + 0x7F7Fu) & 0x8080u));   // bit 7 of each byte kept only where the magnitude is nonzero
+}
+typedef float v2f __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v2f e4m3_unpack2(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false); }
+
 // ------------------------------------------------------------------ the specified sigmoid
 // exp(x) for |x| <= 200: Cody-Waite reduction by ln 2 (fdlibm split) and a degree-13 Taylor polynomial in
 // Horner form, every step one correctly rounded IEEE double operation (no contraction), so the result is

@@ -284,27 +284,19 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
         // the wave's 32 outputs of this route are one E8M0 block of h: max over b and the 16 lanes of the row
         const float am = dpp_group_max16(fmaxf(fabsf(hv[0]), fabsf(hv[1])));
         const int X = fp8_block_exp(am);
-        uint32_t hc[2], lc[2];
-        float res[2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          float dec;
-          hc[b] = e4m3_encode(hv[b], X, &dec);
-          res[b] = hv[b] - dec;
-        }
+        // hi = E4M3 of hv / 2^X, lo = E4M3 of the exact residual / 2^Yx (scalings by powers of two are exact)
+        const uint32_t hc = e4m3_pack2(hv[0] * exp2i(-X), hv[1] * exp2i(-X));
+        const v2f hd = e4m3_unpack2(hc);
+        const float res[2] = {hv[0] - hd.x * exp2i(X), hv[1] - hd.y * exp2i(X)};
         const float ram = dpp_group_max16(fmaxf(fabsf(res[0]), fabsf(res[1])));
         const int Yx = fp8_block_exp(ram);
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          float dec;
-          lc[b] = e4m3_encode(res[b], Yx, &dec);
-        }
+        const uint32_t lc = e4m3_pack2(res[0] * exp2i(-Yx), res[1] * exp2i(-Yx));
         const int rl = PF_UNIT * j + 4 * g + q;  // route of the wave's staging
         uint8_t* row = stg + 64 * rl;
-        row[i] = (uint8_t)hc[0];
-        row[16 + i] = (uint8_t)hc[1];
-        row[32 + i] = (uint8_t)lc[0];
-        row[48 + i] = (uint8_t)lc[1];
+        row[i] = (uint8_t)hc;
+        row[16 + i] = (uint8_t)(hc >> 8);
+        row[32 + i] = (uint8_t)lc;
+        row[48 + i] = (uint8_t)(lc >> 8);
         if (i == 0) {
           ssc[2 * rl] = (uint8_t)(X + 127);
           ssc[2 * rl + 1] = (uint8_t)(Yx + 127);
