@@ -12,13 +12,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // ------------------------------------------------------------------ bf16
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// round-to-nearest-even float -> bf16 bits; NaN stays a quiet NaN
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t n = (u >> 16) | 0x40u;
-  return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? n : r);
-}
+// round-to-nearest-even float -> bf16 bits; NaN stays a quiet NaN with its high payload bits, i.e.
+// ((u + 0x7FFF + ((u >> 16) & 1)) >> 16 for numbers, (u >> 16) | 0x40 for NaN.  The hardware conversion
+// (v_cvt_pk_bf16_f32) gives exactly these bits for every one of the 2^32 inputs (checked on MI355X).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 // ------------------------------------------------------------------ E2M1 / E8M0
