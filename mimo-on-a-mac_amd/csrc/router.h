@@ -11,8 +11,8 @@ struct RouterSmallArgs {
   const float* bias;       // [E]
   int T, H, E, k, nlog;    // nlog = E logits blocks (set by the launcher)
   float* logits;           // [T, E]
-  float* scores;           // [T, E] sigmoid
-  float* keys;             // [T, E] sigmoid + bias
+  float* scores;           // [T, E] sigmoid (optional)
+  float* keys;             // [T, E] sigmoid + bias (optional)
   uint8_t *xq_hi, *xq_lo, *xq_hs, *xq_ls;   // optional fp8 split of x: [T, H], [T, H/32]
 };
 

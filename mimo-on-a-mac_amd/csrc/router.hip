@@ -153,8 +153,8 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
     const float l = ((part[r][0] + part[r][1]) + part[r][2]) + part[r][3];
     const float s = sigmoid_spec(l);
     a.logits[r * a.E + e] = l;
-    a.scores[r * a.E + e] = s;
-    a.keys[r * a.E + e] = s + a.bias[e];
+    if (a.scores) a.scores[r * a.E + e] = s;
+    if (a.keys) a.keys[r * a.E + e] = s + a.bias[e];
   }
 }
 
@@ -463,7 +463,14 @@ int mimo_router(const uint16_t* x, const uint16_t* Wg, const float* bias, int T,
                MIMO_ERR_SHAPE, "router: need H %% 64 == 0, 1 <= k <= min(16, E), E <= 1024");
   if (T == 0) return MIMO_OK;
   hipStream_t st = as_stream(stream);
-  int rc = launch_router_logits(x, Wg, T, H, E, logits, st);
+  int rc;
+  if (T <= 8 && H <= 4096) {   // decode-sized batches: the fused decode's logits kernel, so both give the same bits
+    RouterSmallArgs ra{};
+    ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = T; ra.H = H; ra.E = E; ra.k = k; ra.logits = logits;
+    rc = launch_router_logits_small(ra, st);
+  } else {
+    rc = launch_router_logits(x, Wg, T, H, E, logits, st);
+  }
   if (rc) return rc;
   return launch_router_select(logits, bias, T, E, k, 1.0f, inds, w, nullptr, nullptr, 0, nullptr, st);
 }

@@ -153,3 +153,39 @@ def prefill_dispatch(slot_inds, n_slots):
     inv = np.empty_like(perm)
     inv[perm] = np.arange(perm.size, dtype=np.int32)
     return perm, offsets, inv
+
+
+def lfu_resolve(state, needed, count=True):
+    """Decayed-LFU slot assignment of cache.py:31-62 for one step.
+
+    state: dict with slot_of [E], expert_in [S], cnt [E] float64, last [E] int64, t (mutated in place).
+    Victim score of an occupied slot: cnt * 1e12 + last; empty slots score -1; slots of needed experts are
+    protected; the len(missing) lowest scores are evicted.  Returns (sorted loaded experts, evicted experts,
+    boundary_tie): boundary_tie is True when the last victim's score equals the next candidate's, where the
+    reference's np.argpartition choice is unspecified (callers compare only tie-free steps)."""
+    needed = np.unique(np.asarray(needed))
+    state["t"] += 1
+    if count:
+        state["cnt"][needed] += 1
+    state["last"][needed] = state["t"]
+    slot_of, exp = state["slot_of"], state["expert_in"]
+    missing = needed[slot_of[needed] < 0]
+    if len(missing) == 0:
+        return [], [], False
+    S = len(exp)
+    score = np.array([-1.0 if exp[s] < 0 else state["cnt"][exp[s]] * 1e12 + state["last"][exp[s]] for s in range(S)])
+    for e in needed:
+        if slot_of[e] >= 0:
+            score[slot_of[e]] = np.inf
+    order = np.argsort(score, kind="stable")
+    victims = order[: len(missing)]
+    tie = len(missing) < S and score[order[len(missing) - 1]] == score[order[len(missing)]] and \
+        score[order[len(missing) - 1]] >= 0
+    evicted = []
+    for e, s in zip(missing, victims):
+        if exp[s] >= 0:
+            evicted.append(int(exp[s]))
+            slot_of[exp[s]] = -1
+        exp[s] = e
+        slot_of[e] = s
+    return sorted(int(e) for e in missing), sorted(evicted), bool(tie)
