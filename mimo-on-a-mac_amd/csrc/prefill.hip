@@ -69,6 +69,7 @@ template <> struct PfShape<true> {
   static constexpr int ACOP = 3, BCOP = 2, ECOP = 7, NJ = 3, CSTEP = 2;
 };
 constexpr int PF_STG = 6144;                         // per-wave output staging after the K loop
+constexpr int PF_GROUP = 4;                          // wide tiles whose blocks of one output block run together
 
 // s_waitcnt vmcnt(n) for the counts of the K loop (0, 5, 5 + 7, 5 + 9); a smaller count only waits longer
 __device__ __forceinline__ void pf_wait(int n) {
@@ -343,8 +344,8 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 }
 
 // One launch covers both tile shapes.  Workgroups go to the 8 XCDs round robin (hardware block b runs on XCD
-// b % 8); XCD x takes the x-th eighth of the wide (tile, output block) list and of the narrow one, output blocks
-// fastest, interleaved in proportion so MFMA-bound wide blocks and HBM-bound narrow blocks run side by side.
+// b % 8); XCD x takes the x-th eighth of the wide (tile, output block) list and of the narrow one (output blocks
+// fastest), interleaved in proportion so MFMA-bound wide blocks and HBM-bound narrow blocks run side by side.
 // The 1-D grid has at least 8 ceil(used / 8) blocks per list; the rest exit at once.
 template <bool GATEUP>
 __global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
@@ -362,10 +363,17 @@ __global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
   if (j >= n) return;
   const int wb = (int)(((long long)j * nWx) / n);           // wide blocks before position j
   if ((int)(((long long)(j + 1) * nWx) / n) > wb) {
-    const int l = x * perW + wb, tile = l / obW;
+    // wide list order: groups of PF_GROUP consecutive tiles (a popular slot's tiles are consecutive), output block,
+    // then tile, so the blocks that run together on an XCD share each weight block between PF_GROUP tiles and each
+    // tile's activations between the group's output blocks; the last group may hold fewer tiles
+    const int l = x * perW + wb;
+    const int nW = __builtin_amdgcn_readfirstlane(hdr.x);
+    const int grp = l / (PF_GROUP * obW), rem = l - grp * PF_GROUP * obW;
+    const int ng = min(PF_GROUP, nW - grp * PF_GROUP);
+    const int ob = rem / ng, tile = grp * PF_GROUP + (rem - ob * ng);
     const int4 tt = a.tiles[1 + tile];
     pf_tile<GATEUP, true>(a, pl, s_tok, __builtin_amdgcn_readfirstlane(tt.x), __builtin_amdgcn_readfirstlane(tt.y),
-                          __builtin_amdgcn_readfirstlane(tt.z - tt.y), l - tile * obW);
+                          __builtin_amdgcn_readfirstlane(tt.z - tt.y), ob);
   } else {
     const int l = x * perS + (j - wb), tile = l / obS;
     const int4 tt = a.tiles[1 + a.wcap + tile];
