@@ -475,7 +475,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only: the MoE block runs on a single MI355X "
-                                   "(multi-GPU sharding is described in DESIGN.md, not implemented)",
+                                   "(multi-GPU sharding is designed, not implemented)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
