@@ -14,7 +14,8 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and the built libmimo_moe.so")
 
 
-@pytest.fixture(scope="session")
+@pytest.fixture
 def rng():
+    """A fresh seeded generator per test: a test's inputs do not depend on which tests ran before it."""
     import numpy as np
     return np.random.default_rng(0)
