@@ -17,6 +17,7 @@
 //   D: lane l holds column l % 16, rows 4g .. 4g+3.
 #include "device.h"
 #include "host.h"
+#include "layer.h"
 #include "router.h"
 #include "routing.h"
 
@@ -45,6 +46,7 @@ struct ExpertsArgs {
   float* rt_uw;
   uint32_t* rt_gidx;
   int32_t *rt_nu, *rt_status;
+  const uint16_t* resid;                    // [M, H] residual stream: y := bf16(resid + y) when given
 };
 
 // A operand (FP8 layout) for K-step k0 from a row of E4M3 codes; zero for padding rows.
@@ -422,6 +424,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
   const uint32_t gi = a.gidx[min(tid, nr - 1)];
   const float wi = a.uw[min(tid, UR - 1)];
   const int U = a.n_unique ? min(*a.n_unique, a.Umax) : a.Umax;
+  // the combine's residual element (thread tid < M * 16: row tid / 16, output m0 + tid % 16) comes in with them
+  const uint16_t rres = (a.resid && tid < a.M * 16) ? a.resid[(size_t)(tid >> 4) * a.H + m0 + (tid & 15)] : (uint16_t)0;
   // first route row of expert j = sum of the earlier experts' counts (counts <= 8: four bit-plane ballots)
   int prefv = 0;
   {
@@ -563,7 +567,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const int row = tid >> 4, mi = tid & 15;
     float accy = 0.0f;
     for (int j = 0; j < a.k; ++j) accy = accy + cterm[(row * a.k + j) * 16 + mi];
-    a.y[(size_t)row * a.H + m0 + mi] = f32_to_bf16(accy);
+    const uint16_t yb = f32_to_bf16(accy);
+    a.y[(size_t)row * a.H + m0 + mi] = a.resid ? residual_bf16(rres, yb) : yb;
   }
 }
 
@@ -759,10 +764,14 @@ size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
   return c.off;
 }
 
-int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
-                    int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
-                    size_t ws_bytes, void* stream) {
-  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
+}  // extern "C"
+
+namespace mimo {
+// The fused decode block on rows x (router logits + hi/lo split, experts, combine); resid: optional residual
+// stream added in the combine.
+static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
+                       int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
+                       const uint16_t* resid, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_decode: null pointer");
@@ -780,7 +789,6 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
                &gidx, &nu, &status);
   ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_decode: workspace too small (need %zu)", c.off);
-  hipStream_t st = as_stream(stream);
 
   RouterSmallArgs ra{};
   ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = M; ra.H = H; ra.E = E; ra.k = k;
@@ -802,8 +810,48 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
   a.w_out = w_out ? w_out : w;
   a.rt_uids = uids; a.rt_urows = urows; a.rt_ucnt = ucnt; a.rt_uw = uw; a.rt_gidx = gidx; a.rt_nu = nu;
   a.rt_status = status;
+  a.resid = resid;
   // M == 1 follows _gather_m1 (bf16 expert outputs, model.py:173-182); M >= 2 the distinct-expert kernels
   return run_experts(a, M, M == 1 ? 1 : 0, st);
+}
+}  // namespace mimo
+
+extern "C" {
+
+int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
+                    int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
+                    size_t ws_bytes, void* stream) {
+  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
+  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, ws, ws_bytes,
+                     as_stream(stream));
+}
+
+// The normalised rows r (M x H bf16) go first in the layer workspace, 256-byte aligned.
+static size_t layer_rows_bytes(int M, int H) { return ((size_t)M * H * 2 + 255) / 256 * 256; }
+
+size_t mimo_moe_layer_decode_workspace_size(int M, int E, int k, int H, int I) {
+  return layer_rows_bytes(M, H) + mimo_moe_decode_workspace_size(M, E, k, H, I);
+}
+
+int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
+                          const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank, uint16_t* h,
+                          uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws, size_t ws_bytes, void* stream) {
+  ProfChain chain;
+  MIMO_REQUIRE(x && norm_w && h && bank, MIMO_ERR_ARG, "moe_layer_decode: null pointer");
+  MIMO_REQUIRE(M >= 1 && M <= 8, MIMO_ERR_SHAPE, "moe_layer_decode: need 1 <= M <= 8");
+  MIMO_REQUIRE(aligned16(x) && aligned16(h) && (!r_out || aligned16(r_out)), MIMO_ERR_ALIGN,
+               "moe_layer_decode: 16-byte alignment");
+  MIMO_REQUIRE(r_out != x && r_out != h, MIMO_ERR_ARG, "moe_layer_decode: r_out may not alias x or h");
+  const int H = bank->hidden;
+  const size_t rb = layer_rows_bytes(M, H);
+  MIMO_REQUIRE(ws && ws_bytes >= rb, MIMO_ERR_WORKSPACE, "moe_layer_decode: workspace too small (need %zu)",
+               mimo_moe_layer_decode_workspace_size(M, E, k, H, bank->inter));
+  hipStream_t st = as_stream(stream);
+  uint16_t* r = r_out ? r_out : static_cast<uint16_t*>(ws);
+  int rc = launch_rmsnorm(x, M, H, norm_w, eps, r, st);
+  if (rc) return rc;
+  return decode_impl(r, M, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x, static_cast<uint8_t*>(ws) + rb,
+                     ws_bytes - rb, st);
 }
 
 }  // extern "C"

@@ -13,6 +13,7 @@
 // tile.  The epilogue stages results in LDS and writes 16-byte pieces.
 #include "device.h"
 #include "host.h"
+#include "layer.h"
 #include "router.h"
 
 namespace mimo {
@@ -386,7 +387,7 @@ __global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
 // y[t] = bf16(sum_j fp32(Y[inv[t*k + j]]) * w[t, j]), j ascending (model.py:269-271).
 __global__ void __launch_bounds__(256) prefill_combine_kernel(const uint16_t* __restrict__ Y, const int32_t* __restrict__ inv,
                                                               const float* __restrict__ w, int k, int H,
-                                                              uint16_t* __restrict__ y) {
+                                                              const uint16_t* resid, uint16_t* y) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
   const int m = (blockIdx.x * 256 + threadIdx.x) * 4;
@@ -404,9 +405,19 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(const uint16_t* __
       acc[q] = acc[q] + prod;
     }
   }
+  uint16_t yb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) yb[q] = f32_to_bf16(acc[q]);
+  if (resid) {                       // h = x + y of the decoder layer (resid may alias y: read before the write)
+    const uint2 rv = *reinterpret_cast<const uint2*>(resid + (size_t)t * H + m);
+    yb[0] = residual_bf16((uint16_t)rv.x, yb[0]);
+    yb[1] = residual_bf16((uint16_t)(rv.x >> 16), yb[1]);
+    yb[2] = residual_bf16((uint16_t)rv.y, yb[2]);
+    yb[3] = residual_bf16((uint16_t)(rv.y >> 16), yb[3]);
+  }
   uint2 o;
-  o.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
-  o.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+  o.x = (uint32_t)yb[0] | ((uint32_t)yb[1] << 16);
+  o.y = (uint32_t)yb[2] | ((uint32_t)yb[3] << 16);
   *reinterpret_cast<uint2*>(y + (size_t)t * H + m) = o;
 }
 
@@ -466,7 +477,7 @@ static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int 
 __global__ void reset_status_kernel(int32_t* status) { status[0] = 0; }
 
 static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* wts, int k, const mimo_bank* bank,
-                       uint16_t* y, const PrefillWs& ws, hipStream_t st) {
+                       uint16_t* y, const PrefillWs& ws, hipStream_t st, const uint16_t* resid = nullptr) {
   const int H = bank->hidden, I = bank->inter, S = bank->n_slots;
   const int P = T * k;
   // the GEMM kernels address activation and h rows with 32-bit offsets
@@ -513,7 +524,7 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   { ProfScope p(st, "prefill_gateup"); prefill_gemm_kernel<true><<<grid_gu, 512, PF_LDS, st>>>(a); }
   { ProfScope p(st, "prefill_down"); prefill_gemm_kernel<false><<<grid_dn, 512, PF_LDS, st>>>(a); }
   { ProfScope p(st, "prefill_combine");
-    prefill_combine_kernel<<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, y); }
+    prefill_combine_kernel<<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, resid, y); }
   return check_launch("moe prefill");
 }
 
@@ -564,10 +575,13 @@ size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, i
   return c.off;
 }
 
-int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
-                           int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
-                           size_t ws_bytes, void* stream) {
-  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
+}  // extern "C"
+
+namespace mimo {
+// Router + grouped GEMMs + combine on rows x; resid: optional residual stream added in the combine.
+static int prefill_block_impl(const uint16_t* x, int T, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
+                              int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
+                              const uint16_t* resid, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = check_prefill_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_prefill_block: null pointer");
@@ -577,7 +591,6 @@ int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const f
   Carve c(ws, ws_bytes);
   PrefillWs pw = carve_prefill(c, T, k, bank->n_slots, bank->hidden, bank->inter, E);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill_block: workspace too small (need %zu)", c.off);
-  hipStream_t st = as_stream(stream);
   int32_t* inds = inds_out ? inds_out : pw.inds;
   float* wts = w_out ? w_out : pw.w;
   reset_status_kernel<<<1, 1, 0, st>>>(pw.status);
@@ -586,7 +599,46 @@ int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const f
   rc = launch_router_select(pw.logits, bias, T, E, k, 1.0f, inds, wts, slot_of, pw.slot_inds, bank->n_slots, pw.status,
                             st);
   if (rc) return rc;
-  return run_prefill(x, T, pw.slot_inds, wts, k, bank, y, pw, st);
+  return run_prefill(x, T, pw.slot_inds, wts, k, bank, y, pw, st, resid);
+}
+}  // namespace mimo
+
+extern "C" {
+
+int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
+                           int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
+                           size_t ws_bytes, void* stream) {
+  ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
+  return prefill_block_impl(x, T, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, ws, ws_bytes,
+                            as_stream(stream));
+}
+
+// The normalised rows r (T x H bf16) go first in the layer workspace, 256-byte aligned.
+static size_t prefill_rows_bytes(int T, int H) { return ((size_t)T * H * 2 + 255) / 256 * 256; }
+
+size_t mimo_moe_layer_prefill_workspace_size(int T, int E, int k, int n_slots, int H, int I) {
+  return prefill_rows_bytes(T, H) + mimo_moe_prefill_block_workspace_size(T, E, k, n_slots, H, I);
+}
+
+int mimo_moe_layer_prefill(const uint16_t* x, int T, const uint16_t* norm_w, float eps, const uint16_t* Wg,
+                           const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank, uint16_t* h,
+                           uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws, size_t ws_bytes, void* stream) {
+  ProfChain chain;
+  MIMO_REQUIRE(x && norm_w && h && bank, MIMO_ERR_ARG, "moe_layer_prefill: null pointer");
+  MIMO_REQUIRE(T >= 1, MIMO_ERR_SHAPE, "moe_layer_prefill: need T >= 1");
+  MIMO_REQUIRE(aligned16(x) && aligned16(h) && (!r_out || aligned16(r_out)), MIMO_ERR_ALIGN,
+               "moe_layer_prefill: 16-byte alignment");
+  MIMO_REQUIRE(r_out != x && r_out != h, MIMO_ERR_ARG, "moe_layer_prefill: r_out may not alias x or h");
+  const int H = bank->hidden;
+  const size_t rb = prefill_rows_bytes(T, H);
+  MIMO_REQUIRE(ws && ws_bytes >= rb, MIMO_ERR_WORKSPACE, "moe_layer_prefill: workspace too small (need %zu)",
+               mimo_moe_layer_prefill_workspace_size(T, E, k, bank->n_slots, H, bank->inter));
+  hipStream_t st = as_stream(stream);
+  uint16_t* r = r_out ? r_out : static_cast<uint16_t*>(ws);
+  int rc = launch_rmsnorm(x, T, H, norm_w, eps, r, st);
+  if (rc) return rc;
+  return prefill_block_impl(r, T, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x,
+                            static_cast<uint8_t*>(ws) + rb, ws_bytes - rb, st);
 }
 
 }  // extern "C"

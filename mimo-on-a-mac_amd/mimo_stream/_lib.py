@@ -54,6 +54,12 @@ SIGNATURES = {
     "mimo_moe_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "mimo_moe_prefill_block": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, SZ, P]),
     "mimo_moe_prefill_block_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "mimo_rmsnorm": (I32, [P, I32, I32, P, F32, P, P]),
+    "mimo_residual_add": (I32, [P, P, I64, P, P]),
+    "mimo_moe_layer_decode": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
+    "mimo_moe_layer_decode_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
+    "mimo_moe_layer_prefill": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
+    "mimo_moe_layer_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "mimo_profile_enable": (I32, [I32]),
     "mimo_profile_read": (I32, [I32, P, P, P]),
 }

@@ -96,6 +96,20 @@ class StreamedMoEBlock:
         tab.numpy()[:] = self.cache.slot_of
         self.block.slot_of.copy_(tab, non_blocking=True)
 
+    def prefetch(self, experts):
+        """Predicted experts of a coming step (model.py:320-329): the ones not resident get slots in the same
+        eviction order, without counting as uses (resolve(count=False, stats=False)); their bytes are read now and
+        copied on the side stream after the work already queued, so the reads overlap the GPU work queued before
+        this call.  At most n_slots experts (the first ids given).  Returns the number of experts read."""
+        ids = np.unique(np.asarray(experts, dtype=np.int64).reshape(-1))[: self.cache.S]
+        if ids.size == 0:
+            return 0
+        loads = self.cache.resolve(ids, count=False, stats=False)
+        self._fill(self.block.bank, loads)
+        if loads:
+            self._push_table()
+        return len(loads)
+
     # ---------------------------------------------------------------- forward
     def __call__(self, r, return_routes=False):
         r2 = r.reshape(-1, r.shape[-1]).to(torch.bfloat16).contiguous()

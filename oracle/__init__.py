@@ -12,6 +12,7 @@ Modules:
              the prefill stable dispatch permutation.
   experts  - Kernel A / Kernel B semantics (bf16 rounding points), the M=1 gather_qmm path, the prefill
              pair path and the fixed-order combine.
+  layer    - the decoder layer around the block: post-attention RMSNorm and the residual h = x + y.
 
 Parity status per function is stated in each function's docstring ("pinned by ...").
 """
