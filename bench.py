@@ -10,7 +10,8 @@ of a HIP graph holding exactly --steps steps, inputs resident in HBM.
 
 Also reported (field "extra"): decode at 2, 4, 8 rows with controlled routing (consecutive rows share ~2.6
 of 8 experts), prefill at 512 / 2048 tokens with Zipf(1.1) expert popularity, a 48-layer stack decode at 1
-and 4 rows, and the per-kernel durations measured with HIP events.  "cpu_baseline" times the numpy oracle
+and 4 rows, the MoE half of a decoder layer (post-attention RMSNorm + block + residual) against the block alone
+at 1 row and 2048 tokens, and the per-kernel durations measured with HIP events.  "cpu_baseline" times the numpy oracle
 (the CPU restatement of the reference algorithm) on a bounded sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 500] [--warmup 20]
@@ -461,6 +462,29 @@ def mfma_parse(pmc_dir, trace_dir):
               f"{issued:.0f} | {issued / 2:.0f} | {busy / inst:.1f} | {grbm / (d * 1e6):.0f} |")
 
 
+def layer_case(layers, T, steps, warmup, seed, device):
+    """The MoE half of a decoder layer (post-attention RMSNorm, block, residual added in the combine) against the
+    block alone on the same rows, layers rotated; the difference is what the norm and the residual cost."""
+    import numpy as np
+    import torch
+    from mimo_stream import MoELayer
+    rng = np.random.default_rng(seed)
+    n = len(layers.blocks)
+    nin = min(steps, 64) if T <= 8 else 4
+    if T <= 8:
+        X = np.stack([steered_rows(rng, layers.W[s % n], controlled_sets(rng, T)) for s in range(nin)])
+        Xd = torch.from_numpy(X).to(torch.bfloat16).to(device)
+    else:
+        Xd = torch.randn(nin, T, H, device=device).to(torch.bfloat16)
+    g = torch.Generator(device=device).manual_seed(seed)
+    lays = [MoELayer(b, (1.0 + 0.1 * torch.randn(H, device=device, generator=g)).to(torch.bfloat16), 1e-5)
+            for b in layers.blocks]
+    blocks = layers.blocks
+    ms_l = time_graph(lambda s: lays[s % n](Xd[s % nin]), steps, warmup)
+    ms_b = time_graph(lambda s: blocks[s % n](Xd[s % nin]), steps, warmup)
+    return {"rows": T, "layer_us": ms_l * 1e3, "block_us": ms_b * 1e3, "norm_and_residual_us": (ms_l - ms_b) * 1e3}
+
+
 def main():
     args = parse()
     if args.mfma_parse:
@@ -525,6 +549,13 @@ def main():
                 log(f"[bench] stack M={M}: {r['ms_per_token']:.3f} ms/token, {r['GBps']:.0f} GB/s")
             except Exception as e:
                 extra[f"stack{args.layers}_m{M}"] = {"error": repr(e)}
+        for T, st in ((1, min(args.steps, 300)), (2048, 10)):
+            try:
+                r = layer_case(layers, T, st, 3, seed=40 + T, device=device)
+                extra[f"layer_t{T}"] = r
+                log(f"[bench] layer T={T}: {r['layer_us']:.1f} us (block alone {r['block_us']:.1f} us)")
+            except Exception as e:
+                extra[f"layer_t{T}"] = {"error": repr(e)}
     head.pop("_fn"), head.pop("_U")
     extra["decode_m1"] = head
 

@@ -21,6 +21,9 @@ namespace mimo {
 
 constexpr int kNormMaxPer = 32;   // bf16 elements per thread: H <= 8192
 
+// PER >= H / 256 elements per thread; every load is issued before any is used (indices past the row repeat the
+// thread's first element), so the row arrives in one round trip.
+template <int PER>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict__ x, int H,
                                                       const uint16_t* __restrict__ w, float eps,
                                                       uint16_t* __restrict__ r) {
@@ -30,12 +33,18 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict
   const uint16_t* xr = x + (size_t)blockIdx.x * H;
   uint16_t* rr = r + (size_t)blockIdx.x * H;
   const int n = H >> 8;
-  float xv[kNormMaxPer];
+  uint16_t xb[PER], wb[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = t + 256 * (j < n ? j : 0);
+    xb[j] = xr[e];
+    wb[j] = w[e];
+  }
   float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kNormMaxPer; ++j) {
-    xv[j] = j < n ? bf16_to_f32(xr[t + 256 * j]) : 0.0f;
-    ss = j < n ? ss + xv[j] * xv[j] : ss;
+  for (int j = 0; j < PER; ++j) {
+    const float v = bf16_to_f32(xb[j]);
+    ss = j < n ? ss + v * v : ss;
   }
 #pragma unroll
   for (int s = 32; s >= 1; s >>= 1) ss = ss + __shfl_xor(ss, s, 64);
@@ -44,10 +53,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict
   const float tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
   const float inv = 1.0f / sqrtf(tot / (float)H + eps);
 #pragma unroll
-  for (int j = 0; j < kNormMaxPer; ++j) {
+  for (int j = 0; j < PER; ++j) {
     if (j < n) {
-      const float nv = bf16_to_f32(f32_to_bf16(xv[j] * inv));
-      rr[t + 256 * j] = f32_to_bf16(bf16_to_f32(w[t + 256 * j]) * nv);
+      const float nv = bf16_to_f32(f32_to_bf16(bf16_to_f32(xb[j]) * inv));
+      rr[t + 256 * j] = f32_to_bf16(bf16_to_f32(wb[j]) * nv);
     }
   }
 }
@@ -78,7 +87,16 @@ int launch_rmsnorm(const uint16_t* x, int T, int H, const uint16_t* w, float eps
   MIMO_REQUIRE(T >= 1 && H >= 256 && H % 256 == 0 && H <= 256 * kNormMaxPer, MIMO_ERR_SHAPE,
                "rmsnorm: need T >= 1 and H a multiple of 256 up to %d (got T=%d H=%d)", 256 * kNormMaxPer, T, H);
   MIMO_REQUIRE(eps >= 0.0f && eps == eps, MIMO_ERR_ARG, "rmsnorm: eps must be a non-negative number");
-  { ProfScope p(st, "rmsnorm"); rmsnorm_kernel<<<T, 256, 0, st>>>(x, H, w, eps, r); }
+  const int n = H / 256;
+  {
+    ProfScope p(st, "rmsnorm");
+    if (n <= 1) rmsnorm_kernel<1><<<T, 256, 0, st>>>(x, H, w, eps, r);
+    else if (n <= 2) rmsnorm_kernel<2><<<T, 256, 0, st>>>(x, H, w, eps, r);
+    else if (n <= 4) rmsnorm_kernel<4><<<T, 256, 0, st>>>(x, H, w, eps, r);
+    else if (n <= 8) rmsnorm_kernel<8><<<T, 256, 0, st>>>(x, H, w, eps, r);
+    else if (n <= 16) rmsnorm_kernel<16><<<T, 256, 0, st>>>(x, H, w, eps, r);
+    else rmsnorm_kernel<32><<<T, 256, 0, st>>>(x, H, w, eps, r);
+  }
   return check_launch("rmsnorm");
 }
 

@@ -423,10 +423,98 @@ int launch_router_logits_small(const RouterSmallArgs& args, hipStream_t st) {
   return check_launch("router_logits_small");
 }
 
+// logits[T, E] = x[T, H] . W[E, H]^T on bf16 MFMA (v_mfma_f32_16x16x32_bf16: bf16 products exact in fp32, fp32
+// accumulation), for the prefill chunks (T > 8).  Block (512 threads, 8 waves): 32 tokens x 64 experts; wave w
+// takes K-range w of 8 (H / 8 columns, a multiple of 32) for all of the block's 2 x 4 MFMA tiles, reading its
+// operands straight from global memory: lane (i = l % 16, g = l / 16) of a 16 x 32 step loads 8 consecutive bf16
+// of token row i and of expert row i at columns 8g .. 8g + 7 (the same columns for both operands, so the
+// product pairs them correctly whatever order the unit sums in).  The 8 partial tiles are added in LDS in wave
+// order.  Rows past T or E read the last valid row and are not written.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kRlTok = 32, kRlExp = 64, kRlSplit = 8;
+
+__global__ void __launch_bounds__(512) router_logits_mfma_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ W, int T, int H, int E,
+                                                                 float* __restrict__ logits) {
+  __shared__ float part[kRlSplit][kRlTok][kRlExp];   // 64 KB
+  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t0 = blockIdx.y * kRlTok, e0 = blockIdx.x * kRlExp;
+  const int KW = H / kRlSplit, kb = wave * KW;
+  const uint4* xa[2];
+  const uint4* wb[4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+    xa[a] = reinterpret_cast<const uint4*>(x + (size_t)min(t0 + 16 * a + i, T - 1) * H + kb + 8 * g);
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    wb[b] = reinterpret_cast<const uint4*>(W + (size_t)min(e0 + 16 * b + i, E - 1) * H + kb + 8 * g);
+  v4f acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // 4 K-steps of 32 per round: 24 loads in flight, then 32 MFMAs
+  const int steps = KW / 32;
+  int s = 0;
+  for (; s + 4 <= steps; s += 4) {
+    uint4 av[4][2], bv[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) av[u][a] = xa[a][4 * (s + u)];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) bv[u][b] = wb[b][4 * (s + u)];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[u][a]),
+                                                              __builtin_bit_cast(bf16x8, bv[u][b]), acc[a][b], 0, 0, 0);
+  }
+  for (; s < steps; ++s) {
+    uint4 av[2], bv[4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) av[a] = xa[a][4 * s];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) bv[b] = wb[b][4 * s];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[a]),
+                                                            __builtin_bit_cast(bf16x8, bv[b]), acc[a][b], 0, 0, 0);
+  }
+  // D: lane l holds expert column l % 16 and token rows 4 (l / 16) .. + 3 of each tile
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[wave][16 * a + 4 * g + q][16 * b + i] = acc[a][b][q];
+  __syncthreads();
+  for (int o = threadIdx.x; o < kRlTok * kRlExp; o += 512) {
+    const int r = o / kRlExp, c = o % kRlExp;
+    float v = part[0][r][c];
+#pragma unroll
+    for (int w = 1; w < kRlSplit; ++w) v = v + part[w][r][c];
+    const int t = t0 + r, e = e0 + c;
+    if (t < T && e < E) logits[(size_t)t * E + e] = v;
+  }
+}
+
 int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st) {
-  dim3 grid((E + 63) / 64, (T + 31) / 32);
   ProfScope p(st, "router_logits");
-  router_logits_kernel<<<grid, 256, 0, st>>>(x, W, T, H, E, logits);
+  if (H % (kRlSplit * 32) == 0 && aligned16(x) && aligned16(W)) {
+    dim3 grid((E + kRlExp - 1) / kRlExp, (T + kRlTok - 1) / kRlTok);
+    router_logits_mfma_kernel<<<grid, 512, 0, st>>>(x, W, T, H, E, logits);
+  } else {
+    dim3 grid((E + 63) / 64, (T + 31) / 32);
+    router_logits_kernel<<<grid, 256, 0, st>>>(x, W, T, H, E, logits);
+  }
   return check_launch("router_logits");
 }
 
