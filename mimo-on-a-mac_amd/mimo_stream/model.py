@@ -168,5 +168,10 @@ class MoEBlock:
         return (y, inds, w) if return_routes else y
 
     def forward_residual(self, x, r):
-        """h = x + MoE(r) (model.py:340)."""
-        return x + self(r).reshape(x.shape)
+        """h = x + MoE(r) (model.py:340), the addition in the library (mimo_residual_add: bf16(x + y)).  For the
+        whole MoE half of a layer (norm, block, residual in one call) see mimo_stream.layer.MoELayer."""
+        y = self(r)
+        x2 = x.reshape(y.shape).to(torch.bfloat16).contiguous()
+        h = torch.empty_like(x2)
+        _lib.call("mimo_residual_add", _lib.ptr(x2), _lib.ptr(y), x2.numel(), _lib.ptr(h), _lib.stream_ptr(x2.device))
+        return h.reshape(x.shape)
