@@ -92,6 +92,14 @@ int mimo_sigmoid_table(uint16_t* out, void* stream);
 int mimo_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling,
                        int32_t* inds, float* w, void* stream);
 
+/* group_expert_select of the vendored noaux-tc gate (mimo_v2.py:165-193), given fp32 logits [T, E]: keys =
+ * sigmoid + bias; with n_group > 1 the keys of all but the topk_group groups with the largest sum of their two
+ * largest keys are set to 0 (ties to the lower group index); top-k of the keys; weights = the sigmoid scores
+ * of the chosen experts, renormalised when norm_topk_prob and k > 1, times routed_scaling_factor. */
+int mimo_router_select_grouped(const float* logits, const float* bias, int T, int E, int k, int n_group,
+                               int topk_group, int norm_topk_prob, float routed_scaling_factor, int32_t* inds,
+                               float* w, void* stream);
+
 /* Router.__call__ (model.py:58-65): logits = x.f32 @ Wg.f32^T then mimo_router_select.
  * x bf16 [T, H], Wg bf16 [E, H], bias fp32 [E]; logits fp32 [T, E] (output). */
 int mimo_router(const uint16_t* x, const uint16_t* Wg, const float* bias, int T, int H, int E, int k,

@@ -268,6 +268,69 @@ __global__ void __launch_bounds__(256) router_select_kernel(const float* __restr
   }
 }
 
+// Group-limited selection of the vendored noaux-tc gate (engine/mimo_stream/mimo_v2.py:165-193), one wave per
+// row: s = sigmoid(logit), key = s + bias; with n_group > 1 the experts split into n_group consecutive groups of
+// G = E / n_group, a group's score is the sum of its two largest keys (mx.topk(..., 2), :180), and all but the
+// topk_group highest-scoring groups have their keys set to exactly 0 (:181-185; ties between group scores go to
+// the lower group index, NaN keys never count among a group's two largest); then the top-k of the keys, weights
+// s at the chosen experts renormalised when norm_topk_prob and k > 1 (:190-191), times scaling (:192).
+__global__ void __launch_bounds__(256) router_select_grouped_kernel(const float* __restrict__ logits,
+                                                                    const float* __restrict__ bias, int T, int E, int k,
+                                                                    int n_group, int topk_group, int norm,
+                                                                    float scaling, int32_t* inds, float* w) {
+  extern __shared__ float sm[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* s_row = sm + wave * 2 * E;
+  float* k_row = s_row + E;
+  __shared__ int sel[4][kSelLds];
+  __shared__ int keep[4][64];
+  __shared__ int32_t oi[4][16];
+  __shared__ float ow[4][16];
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  for (int e = lane; e < E; e += 64) {
+    const float s = sigmoid_spec(logits[(size_t)t * E + e]);
+    s_row[e] = s;
+    k_row[e] = s + bias[e];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (n_group > 1) {
+    const int G = E / n_group;
+    float gs = -__builtin_inff();
+    if (lane < n_group) {          // lane g: the two largest keys of group g, in one pass
+      float m1 = -__builtin_inff(), m2 = -__builtin_inff();
+      for (int e = lane * G; e < (lane + 1) * G; ++e) {
+        const float v = k_row[e];
+        if (v > m1) { m2 = m1; m1 = v; }
+        else if (v > m2) m2 = v;
+      }
+      gs = m1 + m2;
+      gs = gs == gs ? gs : -__builtin_inff();
+    }
+    int rank = 0;                   // groups ahead of this one: higher score, or equal score and lower index
+    for (int h = 0; h < n_group; ++h) {
+      const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs), h));
+      rank += (o > gs || (o == gs && h < lane)) ? 1 : 0;
+    }
+    if (lane < n_group) keep[wave][lane] = rank < topk_group;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    for (int e = lane; e < E; e += 64)
+      if (!keep[wave][e / G]) k_row[e] = 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+  wave_select_row(s_row, k_row, E, k, scaling, oi[wave], ow[wave], sel[wave], norm != 0 && k > 1);
+  if (lane < k) {
+    inds[(size_t)t * k + lane] = oi[wave][lane];
+    w[(size_t)t * k + lane] = ow[wave][lane];
+  }
+}
+
 __global__ void group_routes_kernel(const int32_t* inds, const float* scores, const int32_t* slot_of, int M, int k,
                                     int R, int n_slots, int Umax, int32_t* uids, int32_t* urows, int32_t* ucnt,
                                     float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status) {
@@ -542,6 +605,24 @@ int mimo_router_select(const float* logits, const float* bias, int T, int E, int
   if (T == 0) return MIMO_OK;
   return launch_router_select(logits, bias, T, E, k, scaling, inds, w, nullptr, nullptr, 0, nullptr,
                               as_stream(stream));
+}
+
+int mimo_router_select_grouped(const float* logits, const float* bias, int T, int E, int k, int n_group,
+                               int topk_group, int norm_topk_prob, float scaling, int32_t* inds, float* w,
+                               void* stream) {
+  MIMO_REQUIRE(logits && bias && inds && w, MIMO_ERR_ARG, "router_select_grouped: null pointer");
+  MIMO_REQUIRE(T >= 0 && E >= 1 && E <= 1024 && k >= 1 && k <= 16 && k <= E, MIMO_ERR_SHAPE,
+               "router_select_grouped: need 1 <= k <= min(16, E), E <= 1024");
+  MIMO_REQUIRE(n_group >= 1 && n_group <= 64 && E % n_group == 0 && (n_group == 1 || E / n_group >= 2) &&
+                   topk_group >= 1 && topk_group <= n_group,
+               MIMO_ERR_SHAPE, "router_select_grouped: need n_group <= 64 dividing E into groups of >= 2, "
+               "1 <= topk_group <= n_group");
+  if (T == 0) return MIMO_OK;
+  hipStream_t st = as_stream(stream);
+  ProfScope p(st, "router_select_grouped");
+  router_select_grouped_kernel<<<(T + 3) / 4, 256, 4 * 2 * E * sizeof(float), st>>>(
+      logits, bias, T, E, k, n_group, topk_group, norm_topk_prob, scaling, inds, w);
+  return check_launch("router_select_grouped");
 }
 
 int mimo_router(const uint16_t* x, const uint16_t* Wg, const float* bias, int T, int H, int E, int k, float* logits,

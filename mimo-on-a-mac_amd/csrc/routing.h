@@ -58,9 +58,11 @@ __device__ __forceinline__ void wave_load_keys(const float* key_row, int E, uint
   for (int j = 0; j < PER; ++j) cv[j] = (lane + 64 * j) < E ? key_to_ordered(kv[j]) + 1u : 0u;
 }
 
+// renorm: divide the selected scores by their sum (model.py:64; mimo_v2.py:190-191 only when norm_topk_prob and
+// k > 1); the weights are then multiplied by scaling (mimo_v2.py:192) unless it is 1.
 template <int PER>
 __device__ __forceinline__ void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
-                                                  int32_t* inds_out, float* w_out, int* lds_sel) {
+                                                  int32_t* inds_out, float* w_out, int* lds_sel, bool renorm = true) {
   const int lane = threadIdx.x & 63;
   uint32_t* t_key = reinterpret_cast<uint32_t*>(lds_sel);        // [16] selected, in (j, lane) order
   int* t_id = lds_sel + 16;
@@ -121,7 +123,7 @@ __device__ __forceinline__ void wave_select_row_t(const float* s_row, const floa
   denom = __shfl(denom, 0, 64);
   if (lane < k) {
 #pragma clang fp contract(off)
-    float wv = f_sc[lane] / denom;
+    float wv = renorm ? f_sc[lane] / denom : f_sc[lane];
     if (scaling != 1.0f) wv = wv * scaling;
     inds_out[lane] = f_id[lane];
     w_out[lane] = wv;
@@ -130,12 +132,12 @@ __device__ __forceinline__ void wave_select_row_t(const float* s_row, const floa
 }
 
 __device__ __forceinline__ void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,
-                                       int32_t* inds_out, float* w_out, int* lds_sel) {
-  if (E <= 64) wave_select_row_t<1>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
-  else if (E <= 128) wave_select_row_t<2>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
-  else if (E <= 256) wave_select_row_t<4>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
-  else if (E <= 512) wave_select_row_t<8>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
-  else wave_select_row_t<16>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel);
+                                       int32_t* inds_out, float* w_out, int* lds_sel, bool renorm = true) {
+  if (E <= 64) wave_select_row_t<1>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel, renorm);
+  else if (E <= 128) wave_select_row_t<2>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel, renorm);
+  else if (E <= 256) wave_select_row_t<4>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel, renorm);
+  else if (E <= 512) wave_select_row_t<8>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel, renorm);
+  else wave_select_row_t<16>(s_row, key_row, E, k, scaling, inds_out, w_out, lds_sel, renorm);
 }
 
 // ------------------------------------------------------------------ grouping (one wave, <= 64 routes)

@@ -43,6 +43,7 @@ SIGNATURES = {
     "mimo_sigmoid_table": (I32, [P, P]),
     "mimo_router_select": (I32, [P, P, I32, I32, I32, F32, P, P, P]),
     "mimo_router": (I32, [P, P, P, I32, I32, I32, I32, P, P, P, P]),
+    "mimo_router_select_grouped": (I32, [P, P, I32, I32, I32, I32, I32, I32, F32, P, P, P]),
     "mimo_group_routes": (I32, [P, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, P]),
     "mimo_prefill_dispatch": (I32, [P, I32, I32, I32, P, P, P, P, SZ, P]),
     "mimo_prefill_dispatch_workspace_size": (SZ, [I32, I32, I32]),

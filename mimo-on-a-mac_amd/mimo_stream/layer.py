@@ -10,8 +10,9 @@ layer's residual x) and, for layers that keep fewer slots than experts, the pref
 
 A resident block (MoEBlock) runs the whole layer as one library call, mimo_moe_layer_decode (T <= 8) or
 mimo_moe_layer_prefill: the norm kernel, the block on r, and the residual added in the block's combine kernel.  A
-streamed block (StreamedMoEBlock) needs the routes on the host between router and experts, so it runs
-mimo_rmsnorm, the block, then mimo_residual_add.
+streamed block (StreamedMoEBlock) needs the routes on the host between router and experts, and a router with the
+vendored gate's options routes through its own selection, so those run mimo_rmsnorm, the block, then
+mimo_residual_add.
 """
 import json
 import os
@@ -65,7 +66,7 @@ class MoELayer:
         x2 = self._rows(x)
         T = x2.shape[0]
         dev = x2.device
-        if isinstance(self.block, StreamedMoEBlock):
+        if isinstance(self.block, StreamedMoEBlock) or self._inner.router.gate_options is not None:
             r = self.norm(x2)
             y, inds, w = self.block(r, return_routes=True)
             h = torch.empty_like(x2)

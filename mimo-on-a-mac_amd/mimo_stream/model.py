@@ -17,12 +17,26 @@ from .pools import E, TOPK, VERIFY_MAX, bank_struct
 
 
 class Router:
-    """Router (model.py:52-65): weight bf16 [E, H], e_score_correction_bias fp32 [E]."""
+    """Router (model.py:52-65): weight bf16 [E, H], e_score_correction_bias fp32 [E].
 
-    def __init__(self, hidden, n_experts=E, top_k=TOPK, device="cuda"):
+    The defaults are the engine's router (renormalised weights for every k).  The options of the vendored
+    noaux-tc gate (MoEGate, mimo_v2.py:195-216) apply when set: group-limited selection (n_group > 1,
+    topk_group), norm_topk_prob (renormalise only when set and k > 1) and routed_scaling_factor; the routes then
+    come from mimo_router_select_grouped, and blocks run their experts on the given routes."""
+
+    def __init__(self, hidden, n_experts=E, top_k=TOPK, device="cuda", n_group=None, topk_group=None,
+                 norm_topk_prob=None, routed_scaling_factor=None):
         self.weight = torch.zeros((n_experts, hidden), dtype=torch.bfloat16, device=device)
         self.e_score_correction_bias = torch.zeros(n_experts, dtype=torch.float32, device=device)
         self.top_k = top_k
+        self.gate_options = None
+        if any(v is not None for v in (n_group, topk_group, norm_topk_prob, routed_scaling_factor)):
+            ng = 1 if n_group is None else int(n_group)
+            tg = ng if topk_group is None else int(topk_group)
+            if ng < 1 or n_experts % ng or not 1 <= tg <= ng:
+                raise ValueError("need n_group dividing the experts and 1 <= topk_group <= n_group")
+            self.gate_options = (ng, tg, True if norm_topk_prob is None else bool(norm_topk_prob),
+                                 1.0 if routed_scaling_factor is None else float(routed_scaling_factor))
 
     def logits_and_routes(self, r):
         """r bf16 [..., T, H] -> (logits fp32 [T, E], inds int32 [T, k], w fp32 [T, k])."""
@@ -37,6 +51,10 @@ class Router:
         _lib.call("mimo_router", _lib.ptr(r2), _lib.ptr(self.weight.contiguous()),
                   _lib.ptr(self.e_score_correction_bias.contiguous()), T, H, En, self.top_k, _lib.ptr(logits),
                   _lib.ptr(inds), _lib.ptr(w), _lib.stream_ptr(dev))
+        if self.gate_options is not None:
+            ng, tg, norm, scale = self.gate_options
+            _lib.call("mimo_router_select_grouped", _lib.ptr(logits), _lib.ptr(self.e_score_correction_bias.contiguous()),
+                      T, En, self.top_k, ng, tg, int(norm), scale, _lib.ptr(inds), _lib.ptr(w), _lib.stream_ptr(dev))
         return logits, inds, w
 
     def __call__(self, r):
@@ -150,6 +168,10 @@ class MoEBlock:
         dev = r2.device
         b = self._bank_struct
         rt = self.router
+        if rt.gate_options is not None:     # the vendored gate's options: route, then the experts on the routes
+            inds, w = rt(r2)
+            y = self._moe_small(r2, inds, w) if T <= VERIFY_MAX else self._moe_prefill(r2, inds, w)
+            return (y, inds, w) if return_routes else y
         En, k = rt.weight.shape[0], rt.top_k
         y = torch.empty((T, b.hidden), dtype=torch.bfloat16, device=dev)
         inds = torch.empty((T, k), dtype=torch.int32, device=dev)

@@ -2,7 +2,8 @@
 
 Reference functions restated here:
   * Router.__call__            engine/mimo_stream/model.py:58-65
-  * group_expert_select        engine/mimo_stream/mimo_v2.py:165-193 (n_group == 1 branch; scaling factor)
+  * group_expert_select        engine/mimo_stream/mimo_v2.py:165-193 (select_topk: n_group == 1 with
+                               renormalisation; select_topk_grouped: every option of the vendored gate)
   * SlotCache.slot_of          engine/mimo_stream/cache.py:16-17, :24-29 (expert -> slot)
   * group_routes               engine/mimo_stream/kernels.py:149-173
   * _moe_prefill dispatch      engine/mimo_stream/model.py:235-242, :266-268 (stable sort by slot, inverse)
@@ -89,6 +90,59 @@ def select_topk(logits, bias, k, routed_scaling_factor=1.0):
         w[t] = (s[t, sel] / denom).astype(np.float32)
         if routed_scaling_factor != 1.0:
             w[t] = (w[t] * np.float32(routed_scaling_factor)).astype(np.float32)
+    return inds, w
+
+
+def group_mask_keys(key, n_group, topk_group):
+    """mimo_v2.py:178-186 on one row of fp32 keys [E]: the experts split into n_group consecutive groups; a
+    group's score is the fp32 sum of its two largest keys (mx.topk(scores, 2)); every group outside the
+    topk_group highest scores has its keys set to 0.0.  Fixed here where MLX leaves it open: ties between group
+    scores go to the lower group index; NaN keys never count among a group's two largest (a group with fewer
+    than two non-NaN keys scores -inf), and a NaN score ranks lowest."""
+    key = np.asarray(key, np.float32)
+    E = key.shape[0]
+    G = E // n_group
+    scores = np.empty(n_group, np.float32)
+    for g in range(n_group):
+        v = key[g * G:(g + 1) * G]
+        v = np.sort(v[~np.isnan(v)])[::-1]
+        top = list(v[:2]) + [np.float32(-np.inf)] * (2 - min(2, len(v)))
+        sc = np.float32(np.float32(top[0]) + np.float32(top[1]))
+        scores[g] = -np.inf if np.isnan(sc) else sc
+    order = np.lexsort((np.arange(n_group), -scores))        # score descending, lower index first
+    out = key.copy()
+    for g in order[topk_group:]:
+        out[g * G:(g + 1) * G] = np.float32(0.0)
+    return out
+
+
+def select_topk_grouped(logits, bias, k, n_group=1, topk_group=1, norm_topk_prob=True, routed_scaling_factor=1.0):
+    """group_expert_select (mimo_v2.py:165-193) given fp32 logits [T, E]: s = sigmoid_f32(logits); key = s + bias;
+    with n_group > 1 the group mask of group_mask_keys; canonical order of the keys (descending, ties to the
+    lower id, NaN last); w = s at the chosen experts, divided by (their sum in selection order + 1e-20f) only when
+    norm_topk_prob and k > 1 (:190-191), times routed_scaling_factor (:192)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    s = sigmoid_f32(logits)
+    key = (s + np.asarray(bias, dtype=np.float32)[None, :]).astype(np.float32)
+    inds = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    ids = np.arange(E)
+    for t in range(T):
+        kt = group_mask_keys(key[t], n_group, topk_group) if n_group > 1 else key[t]
+        nan = np.isnan(kt)
+        order = np.lexsort((ids, -np.where(nan, 0, kt), nan))
+        sel = order[:k]
+        inds[t] = sel
+        wt = s[t, sel].astype(np.float32)
+        if norm_topk_prob and k > 1:
+            acc = np.float32(0.0)
+            for j in range(k):
+                acc = np.float32(acc + wt[j])
+            wt = (wt / np.float32(acc + np.float32(1e-20))).astype(np.float32)
+        if routed_scaling_factor != 1.0:
+            wt = (wt * np.float32(routed_scaling_factor)).astype(np.float32)
+        w[t] = wt
     return inds, w
 
 
