@@ -348,13 +348,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
     float amax = dpp_group_max16(fabsf(v));
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     const int X = fp8_block_exp(amax);
-    float dec;
-    const uint32_t hc = e4m3_encode(v, X, &dec);
-    const float res = v - dec;
+    float res;
+    const uint32_t hc = e4m3_encode(v, X, &res);
     float ramax = dpp_group_max16(fabsf(res));
     ramax = fmaxf(ramax, __shfl_xor(ramax, 16, 64));
     const int Y = fp8_block_exp(ramax);
-    const uint32_t lc = e4m3_encode(res, Y, &dec);
+    float lres;   // the lo code's own residual, unused
+    const uint32_t lc = e4m3_encode(res, Y, &lres);
     if (r < cnt) {
       const size_t row = (size_t)u * a.R + r;
       a.hq_hi[row * a.I + nb + nl] = (uint8_t)hc;

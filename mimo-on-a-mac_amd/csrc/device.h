@@ -67,14 +67,16 @@ __device__ __forceinline__ int fp8_block_exp(float amax) {
 __device__ __forceinline__ float exp2i(int X) {   // 2^X for -127 <= X <= 127, exact
   return X >= -126 ? __uint_as_float((uint32_t)(X + 127) << 23) : __uint_as_float(0x00400000u);
 }
-// Signed E4M3 code of v / 2^X (positive zero for a zero magnitude); returns code, writes decoded value.
-__device__ __forceinline__ uint32_t e4m3_encode(float v, int X, float* dec) {
+// Signed E4M3 code of v / 2^X (positive zero for a zero magnitude); writes the residual v - code * 2^X, computed
+// as one fused multiply-add: the difference is exact and the product, which can pass the fp32 range for the
+// largest blocks (448 * 2^120), is never rounded on its own.
+__device__ __forceinline__ uint32_t e4m3_encode(float v, int X, float* res) {
   float inv = exp2i(-X);        // exact when -X in range; X >= -127 so -X <= 127
   float y = fabsf(v) * inv;
   uint32_t mag = e4m3_mag_code(y);
-  float dv = e4m3_decode_mag(mag) * exp2i(X);
+  float dm = e4m3_decode_mag(mag);
   uint32_t sgn = (mag != 0u && v < 0.0f) ? 0x80u : 0u;
-  *dec = sgn ? -dv : dv;
+  *res = __builtin_fmaf(sgn ? dm : -dm, exp2i(X), v);
   return mag | sgn;
 }
 
@@ -130,40 +132,38 @@ __device__ __forceinline__ float sigmoid_spec(float xf) {
   return nan ? __uint_as_float(0x7FC00000u) : s;
 }
 
-// 32 bf16-valued floats -> hi / lo E4M3 words (4 codes per word, element order) and E8M0 bytes:
-// hi = E4M3 block quantisation of v, lo = the same of the exact residual v - hi.
+// 32 bf16-valued floats -> hi / lo E4M3 words (4 codes per word, element order) and E8M0 bytes: hi = E4M3 block
+// quantisation of v, lo = the same of the exact residual v - hi.  Codes from the hardware conversion
+// (v_cvt_pk_fp8_f32: OCP E4M3, round to nearest even, checked against e4m3_encode on every bf16 input;
+// e4m3_pack2 clears the sign of zero codes); the scalings by 2^-X and 2^-Y are exact, and the residual is one
+// fused multiply-add (exact, with no overflow of the product for the largest blocks).
 __device__ __forceinline__ void quant_block_fp8_hilo(const float* v, uint32_t* hw, uint32_t* lw, uint8_t* hsb,
-                                                     uint8_t* lsb) {
+                                                        uint8_t* lsb) {
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  int X = fp8_block_exp(amax);
+  const int X = fp8_block_exp(amax);
+  const float sx = exp2i(-X), dx = exp2i(X);
   float r[32];
   float ramax = 0.0f;
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0;
+    const uint32_t c01 = e4m3_pack2(v[4 * w] * sx, v[4 * w + 1] * sx);
+    const uint32_t c23 = e4m3_pack2(v[4 * w + 2] * sx, v[4 * w + 3] * sx);
+    hw[w] = c01 | (c23 << 16);
+    const v2f d01 = e4m3_unpack2(c01), d23 = e4m3_unpack2(c23);
+    r[4 * w] = __builtin_fmaf(-d01.x, dx, v[4 * w]);          // exact residuals, no overflow of the product
+    r[4 * w + 1] = __builtin_fmaf(-d01.y, dx, v[4 * w + 1]);
+    r[4 * w + 2] = __builtin_fmaf(-d23.x, dx, v[4 * w + 2]);
+    r[4 * w + 3] = __builtin_fmaf(-d23.y, dx, v[4 * w + 3]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float dec;
-      uint32_t c = e4m3_encode(v[w * 4 + j], X, &dec);
-      word |= c << (8 * j);
-      r[w * 4 + j] = v[w * 4 + j] - dec;
-      ramax = fmaxf(ramax, fabsf(r[w * 4 + j]));
-    }
-    hw[w] = word;
+    for (int j = 0; j < 4; ++j) ramax = fmaxf(ramax, fabsf(r[4 * w + j]));
   }
-  int Y = fp8_block_exp(ramax);
+  const int Y = fp8_block_exp(ramax);
+  const float sy = exp2i(-Y);
 #pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float dec;
-      word |= e4m3_encode(r[w * 4 + j], Y, &dec) << (8 * j);
-    }
-    lw[w] = word;
-  }
+  for (int w = 0; w < 8; ++w)
+    lw[w] = e4m3_pack2(r[4 * w] * sy, r[4 * w + 1] * sy) | (e4m3_pack2(r[4 * w + 2] * sy, r[4 * w + 3] * sy) << 16);
   *hsb = (uint8_t)(X + 127);
   *lsb = (uint8_t)(Y + 127);
 }

@@ -289,7 +289,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
         // hi = E4M3 of hv / 2^X, lo = E4M3 of the exact residual / 2^Yx (scalings by powers of two are exact)
         const uint32_t hc = e4m3_pack2(hv[0] * exp2i(-X), hv[1] * exp2i(-X));
         const v2f hd = e4m3_unpack2(hc);
-        const float res[2] = {hv[0] - hd.x * exp2i(X), hv[1] - hd.y * exp2i(X)};
+        const float res[2] = {__builtin_fmaf(-hd.x, exp2i(X), hv[0]), __builtin_fmaf(-hd.y, exp2i(X), hv[1])};
         const float ram = dpp_group_max16(fmaxf(fabsf(res[0]), fabsf(res[1])));
         const int Yx = fp8_block_exp(ram);
         const uint32_t lc = e4m3_pack2(res[0] * exp2i(-Yx), res[1] * exp2i(-Yx));

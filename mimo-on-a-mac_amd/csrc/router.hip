@@ -89,13 +89,13 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
     float amax = dpp_group_max16(fabsf(v));
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     const int X = fp8_block_exp(amax);
-    float dec;
-    const uint32_t hc = e4m3_encode(v, X, &dec);
-    const float res = v - dec;
+    float res;
+    const uint32_t hc = e4m3_encode(v, X, &res);
     float ramax = dpp_group_max16(fabsf(res));
     ramax = fmaxf(ramax, __shfl_xor(ramax, 16, 64));
     const int Y = fp8_block_exp(ramax);
-    const uint32_t lc = e4m3_encode(res, Y, &dec);
+    float lres;   // the lo code's own residual, unused
+    const uint32_t lc = e4m3_encode(res, Y, &lres);
     if (live) {
       a.xq_hi[idx] = (uint8_t)hc;
       a.xq_lo[idx] = (uint8_t)lc;

@@ -62,6 +62,24 @@ def test_fp8_hilo_bit_exact(rng):
         np.testing.assert_array_equal(got.cpu().numpy(), ref)
 
 
+def test_fp8_hilo_every_finite_bf16(rng):
+    """Every finite bf16 value, shuffled into 32-element blocks (wide ranges inside a block: subnormal and
+    saturating E4M3 codes, negative values that round to zero), plus blocks mixing 1e30 with tiny values."""
+    from mimo_stream import kernels
+    bits = np.arange(65536, dtype=np.uint32)
+    finite = ((bits >> 7) & 0xFF) != 0xFF
+    vals = ((bits[finite] << 16).astype(np.uint32)).view(np.float32)
+    vals = vals[rng.permutation(vals.size)]
+    n = vals.size // 4096 * 4096
+    x = vals[:n].reshape(-1, 4096).copy()
+    x[0, :32] = oq.round_bf16(np.float32(1e30) * rng.standard_normal(32).astype(np.float32) ** 9)
+    x[0, 32:64] = oq.round_bf16(np.array([-1e-20] * 31 + [3.0], np.float32))
+    hi, hs, lo, ls = kernels.quantize_fp8_hilo(to_dev_bf16(x))
+    ohi, ohs, olo, ols = oq.quantize_fp8_hilo(x)
+    for got, ref in ((hi, ohi), (hs, ohs), (lo, olo), (ls, ols)):
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
 def test_sigmoid_table_bit_exact():
     from mimo_stream import kernels
     tab = bf16_bits(kernels.sigmoid_table())
