@@ -161,16 +161,17 @@ size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, i
 
 /* post_attention_layernorm (model.py:299, nn.RMSNorm(hidden, eps=layernorm_epsilon) :75): r = RMSNorm(x) * w
  * for T rows of H bf16 (H a multiple of 256, at most 8192), fp32 sum of squares in a fixed tree, inv =
- * 1 / sqrt(ss / H + eps), r = bf16(w * bf16(x * inv)).  r may not alias x. */
+ * 1 / sqrt(ss / H + eps), r = bf16(w * bf16(x * inv)).  r may not alias x; x, w, r 16-byte aligned. */
 int mimo_rmsnorm(const uint16_t* x, int T, int H, const uint16_t* w, float eps, uint16_t* r, void* stream);
 
 /* The layer residual h = x + y (model.py:340): h = bf16(x + y) elementwise over n bf16 values; h may alias x or
  * y.  Pointers 16-byte aligned. */
 int mimo_residual_add(const uint16_t* x, const uint16_t* y, int64_t n, uint16_t* h, void* stream);
 
-/* The MoE half of a decoder layer in decode (model.py:299-340 for T <= 8): r = RMSNorm(x) * norm_w, the
- * decode block on r (as mimo_moe_decode), h = bf16(x + y) in the block's combine.  h may alias x; r_out
- * (optional, not aliasing x or h) receives r; inds_out / w_out (optional) the routes. */
+/* The MoE half of a decoder layer in decode (model.py:299-340 for T <= 8): r = RMSNorm(x) * norm_w (computed
+ * inside the router kernel, bit-identical to mimo_rmsnorm), the decode block on r (as mimo_moe_decode),
+ * h = bf16(x + y) in the block's combine.  h may alias x; r_out (optional, not aliasing x or h) receives r;
+ * inds_out / w_out (optional) the routes. */
 int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
                           const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank,
                           uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws,

@@ -185,26 +185,23 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   int U, cnt_raw, slot, tok;          // tok: lane c < R holds the token of the expert's row c
   // one row with expert ids as slots: a block needs only its expert, the u-th selected one in ascending id order
   const bool fast = ROUTED && a.M == 1 && a.slot_of == nullptr && a.S >= a.E;
-  __shared__ int fast_slot[16];
+  const bool publisher = ROUTED && blockIdx.x == 0 && blockIdx.y == 0;
   if (ROUTED && fast) {
     if (wave == 0) {
       uint32_t cv[4];
+      float sc[4];
       bool take[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)                       // the scores only for the block that publishes the routes
+        sc[j] = publisher ? a.scores[(lane + 64 * j) < a.E ? lane + 64 * j : 0] : 0.0f;
       wave_load_keys<4>(a.keys, a.E, cv);              // E <= 256 on this path
       wave_select_set<4>(cv, a.k, take);
-      const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-      int before = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint64_t sel = __ballot(take[j]);
-        if (take[j]) fast_slot[before + __popcll(sel & below)] = lane + 64 * j;
-        before += __popcll(sel);
-      }
+      wave_stage_selected<4>(cv, sc, take, sel[0]);     // ids in ascending order at sel[0][16 ..]
     }
     __syncthreads();
     U = a.k;                                            // distinct experts, one row each
     cnt_raw = 1;
-    slot = u < U ? fast_slot[u] : 0;
+    slot = u < U ? sel[0][16 + u] : 0;
     tok = 0;
   } else if (ROUTED) {
     // routes of this step: wave r selects row r (top-k and renormalisation), wave 0 groups them by slot; every
@@ -260,6 +257,17 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   for (int s = 0; s < NS; ++s) { bg[s] = gw[4 * s]; bu[s] = upw[4 * s]; }
   const uint2 sp0 = *piece_src(q0);
   const uint2 sp1 = *piece_src(q1);
+  __builtin_amdgcn_sched_barrier(0);
+  if (ROUTED && fast && publisher && wave == 0) {
+    // the step's full routing for the down kernel while this block's loads stream: ranking, renormalisation and
+    // grouping of the staged selection touch only LDS and registers (workgroup fences wait on LDS only)
+    wave_rank_renorm(a.k, 1.0f, s_inds, s_w, sel[0], true);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    wave_group_routes(s_inds, s_w, nullptr, 1, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
+                      &g_nu[0], &g_nu[1], lurows, luw);
+  }
   __builtin_amdgcn_sched_barrier(0);
   if (p0 < npieces) *piece_dst(p0) = sp0;
   if (p1 < npieces) *piece_dst(p1) = sp1;
@@ -365,13 +373,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
       }
     }
   }
-  if (ROUTED && blockIdx.x == 0 && blockIdx.y == 0) {   // block (0, 0) publishes the full routing for the down kernel
-    if (fast) {
-      __syncthreads();
-      full_routing(a, sel, s_inds, s_w, lurows, luw, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, wave);
-    }
+  if (publisher)   // block (0, 0) publishes the full routing for the down kernel
     publish_routes(a, s_inds, s_w, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, tid);
-  }
 }
 
 // ------------------------------------------------------------------ Kernel B + combine (owner computes)
@@ -768,10 +771,11 @@ size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
 
 namespace mimo {
 // The fused decode block on rows x (router logits + hi/lo split, experts, combine); resid: optional residual
-// stream added in the combine.
+// stream added in the combine; norm_w: optional RMSNorm of the rows inside the router kernel (r to r_out if given).
 static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
                        int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
-                       const uint16_t* resid, void* ws, size_t ws_bytes, hipStream_t st) {
+                       const uint16_t* resid, const uint16_t* norm_w, float eps, uint16_t* r_out, void* ws,
+                       size_t ws_bytes, hipStream_t st) {
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_decode: null pointer");
@@ -794,6 +798,7 @@ static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float
   ra.x = x; ra.Wg = Wg; ra.bias = bias; ra.T = M; ra.H = H; ra.E = E; ra.k = k;
   ra.logits = logits; ra.scores = scores; ra.keys = keys;
   ra.xq_hi = ew.xq_hi; ra.xq_lo = ew.xq_lo; ra.xq_hs = ew.xq_hs; ra.xq_ls = ew.xq_ls;
+  ra.norm_w = norm_w; ra.eps = eps; ra.r_out = r_out;
   rc = launch_router_logits_small(ra, st);
   if (rc) return rc;
 
@@ -822,15 +827,14 @@ int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* b
                     int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
                     size_t ws_bytes, void* stream) {
   ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
-  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, ws, ws_bytes,
-                     as_stream(stream));
+  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, nullptr, 0.0f, nullptr, ws,
+                     ws_bytes, as_stream(stream));
 }
 
-// The normalised rows r (M x H bf16) go first in the layer workspace, 256-byte aligned.
-static size_t layer_rows_bytes(int M, int H) { return ((size_t)M * H * 2 + 255) / 256 * 256; }
-
+// The layer step normalises the rows inside the router kernel: no rows of r are kept unless r_out asks for them,
+// so the workspace is the decode block's.
 size_t mimo_moe_layer_decode_workspace_size(int M, int E, int k, int H, int I) {
-  return layer_rows_bytes(M, H) + mimo_moe_decode_workspace_size(M, E, k, H, I);
+  return mimo_moe_decode_workspace_size(M, E, k, H, I);
 }
 
 int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
@@ -839,19 +843,12 @@ int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, floa
   ProfChain chain;
   MIMO_REQUIRE(x && norm_w && h && bank, MIMO_ERR_ARG, "moe_layer_decode: null pointer");
   MIMO_REQUIRE(M >= 1 && M <= 8, MIMO_ERR_SHAPE, "moe_layer_decode: need 1 <= M <= 8");
-  MIMO_REQUIRE(aligned16(x) && aligned16(h) && (!r_out || aligned16(r_out)), MIMO_ERR_ALIGN,
+  MIMO_REQUIRE(aligned16(x) && aligned16(h) && aligned16(norm_w) && (!r_out || aligned16(r_out)), MIMO_ERR_ALIGN,
                "moe_layer_decode: 16-byte alignment");
   MIMO_REQUIRE(r_out != x && r_out != h, MIMO_ERR_ARG, "moe_layer_decode: r_out may not alias x or h");
-  const int H = bank->hidden;
-  const size_t rb = layer_rows_bytes(M, H);
-  MIMO_REQUIRE(ws && ws_bytes >= rb, MIMO_ERR_WORKSPACE, "moe_layer_decode: workspace too small (need %zu)",
-               mimo_moe_layer_decode_workspace_size(M, E, k, H, bank->inter));
-  hipStream_t st = as_stream(stream);
-  uint16_t* r = r_out ? r_out : static_cast<uint16_t*>(ws);
-  int rc = launch_rmsnorm(x, M, H, norm_w, eps, r, st);
-  if (rc) return rc;
-  return decode_impl(r, M, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x, static_cast<uint8_t*>(ws) + rb,
-                     ws_bytes - rb, st);
+  MIMO_REQUIRE(eps >= 0.0f && eps == eps, MIMO_ERR_ARG, "moe_layer_decode: eps must be a non-negative number");
+  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x, norm_w, eps, r_out, ws, ws_bytes,
+                     as_stream(stream));
 }
 
 }  // extern "C"

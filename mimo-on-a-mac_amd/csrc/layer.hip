@@ -5,60 +5,45 @@
 // This file holds the RMSNorm kernel and the standalone residual add; the fused layer entry points (norm, block,
 // residual in the combine kernels) sit with the decode and prefill paths.
 //
-// RMSNorm rounding points (one row per 256-thread block, H = 256 n):
-//   ss  = fp32 sum of x^2 (a bf16 square is exact in fp32): thread t adds x[t + 256 j]^2 for j = 0, 1, ... in
-//         order; each wave's 64 partials combine by a butterfly (xor 32, 16, 8, 4, 2, 1); the 4 wave sums as
-//         (s0 + s1) + (s2 + s3)
-//   inv = 1 / sqrt(ss / H + eps)             (IEEE fp32 division and square root)
-//   r_j = bf16(w_j * bf16(x_j * inv))        (normalise, round, scale: the w product is exact in fp32)
-// mlx.core.fast.rms_norm (the reference's nn.RMSNorm) applies the same rounding points with its own fp32 sum
-// order, so the two agree to within a bf16 rounding flip where inv differs in its last bits.
+// RMSNorm: the rounding points and the fp32 summation order are those of layer.h (norm_*).  mlx.core.fast.rms_norm
+// (the reference's nn.RMSNorm) applies the same rounding points with its own fp32 sum order, so the two agree to
+// within a bf16 rounding flip where inv differs in its last bits.
 #include "device.h"
 #include "host.h"
 #include "layer.h"
 
 namespace mimo {
 
-constexpr int kNormMaxPer = 32;   // bf16 elements per thread: H <= 8192
-
-// PER >= H / 256 elements per thread; every load is issued before any is used (indices past the row repeat the
-// thread's first element), so the row arrives in one round trip.
-template <int PER>
+// One row per 256-thread block; NCH = ceil(H / 2048) chunks of 8 elements per thread, all loaded before any is used
+// (a thread's empty chunks re-read its wave's first chunk and are not counted), so the row arrives in one round trip.
+template <int NCH>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict__ x, int H,
                                                       const uint16_t* __restrict__ w, float eps,
                                                       uint16_t* __restrict__ r) {
-#pragma clang fp contract(off)
   __shared__ float wsum[4];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const uint16_t* xr = x + (size_t)blockIdx.x * H;
-  uint16_t* rr = r + (size_t)blockIdx.x * H;
-  const int n = H >> 8;
-  uint16_t xb[PER], wb[PER];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q4 = H >> 2;
+  const size_t rowq = (size_t)blockIdx.x * H + wave * q4;
+  uint4 xv[NCH], wv[NCH];
+  bool ok[NCH];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int e = t + 256 * (j < n ? j : 0);
-    xb[j] = xr[e];
-    wb[j] = w[e];
+  for (int c = 0; c < NCH; ++c) {
+    const int off = c * 512 + 8 * lane;
+    ok[c] = off < q4;
+    const int o = ok[c] ? off : 0;
+    xv[c] = *reinterpret_cast<const uint4*>(x + rowq + o);
+    wv[c] = *reinterpret_cast<const uint4*>(w + wave * q4 + o);
   }
   float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const float v = bf16_to_f32(xb[j]);
-    ss = j < n ? ss + v * v : ss;
-  }
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) ss = ss + __shfl_xor(ss, s, 64);
+  for (int c = 0; c < NCH; ++c) ss = ok[c] ? norm_sq_add8(xv[c], ss) : ss;
+  ss = norm_wave_sum(ss);
   if (lane == 0) wsum[wave] = ss;
   __syncthreads();
-  const float tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+  const float inv = norm_inv(wsum, H, eps);
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    if (j < n) {
-      const float nv = bf16_to_f32(f32_to_bf16(bf16_to_f32(xb[j]) * inv));
-      rr[t + 256 * j] = f32_to_bf16(bf16_to_f32(wb[j]) * nv);
-    }
-  }
+  for (int c = 0; c < NCH; ++c)
+    if (ok[c]) *reinterpret_cast<uint4*>(r + rowq + c * 512 + 8 * lane) = norm_apply8(xv[c], wv[c], inv);
 }
 
 // h = bf16(x + y), 8 elements per thread (n a multiple of 8, 16-byte aligned rows) or one per thread otherwise.
@@ -84,18 +69,19 @@ __global__ void __launch_bounds__(256) residual_add_kernel(const uint16_t* x, co
 
 int launch_rmsnorm(const uint16_t* x, int T, int H, const uint16_t* w, float eps, uint16_t* r, hipStream_t st) {
   MIMO_REQUIRE(x && w && r, MIMO_ERR_ARG, "rmsnorm: null pointer");
-  MIMO_REQUIRE(T >= 1 && H >= 256 && H % 256 == 0 && H <= 256 * kNormMaxPer, MIMO_ERR_SHAPE,
-               "rmsnorm: need T >= 1 and H a multiple of 256 up to %d (got T=%d H=%d)", 256 * kNormMaxPer, T, H);
+  MIMO_REQUIRE(T >= 1 && H >= 256 && H % 256 == 0 && H <= 8192, MIMO_ERR_SHAPE,
+               "rmsnorm: need T >= 1 and H a multiple of 256 up to 8192 (got T=%d H=%d)", T, H);
+  MIMO_REQUIRE(aligned16(x) && aligned16(w) && aligned16(r), MIMO_ERR_ALIGN, "rmsnorm: 16-byte alignment");
   MIMO_REQUIRE(eps >= 0.0f && eps == eps, MIMO_ERR_ARG, "rmsnorm: eps must be a non-negative number");
-  const int n = H / 256;
+  const int nch = (H / 4 + 511) / 512;
   {
     ProfScope p(st, "rmsnorm");
-    if (n <= 1) rmsnorm_kernel<1><<<T, 256, 0, st>>>(x, H, w, eps, r);
-    else if (n <= 2) rmsnorm_kernel<2><<<T, 256, 0, st>>>(x, H, w, eps, r);
-    else if (n <= 4) rmsnorm_kernel<4><<<T, 256, 0, st>>>(x, H, w, eps, r);
-    else if (n <= 8) rmsnorm_kernel<8><<<T, 256, 0, st>>>(x, H, w, eps, r);
-    else if (n <= 16) rmsnorm_kernel<16><<<T, 256, 0, st>>>(x, H, w, eps, r);
-    else rmsnorm_kernel<32><<<T, 256, 0, st>>>(x, H, w, eps, r);
+    switch (nch) {
+      case 1: rmsnorm_kernel<1><<<T, 256, 0, st>>>(x, H, w, eps, r); break;
+      case 2: rmsnorm_kernel<2><<<T, 256, 0, st>>>(x, H, w, eps, r); break;
+      case 3: rmsnorm_kernel<3><<<T, 256, 0, st>>>(x, H, w, eps, r); break;
+      default: rmsnorm_kernel<4><<<T, 256, 0, st>>>(x, H, w, eps, r); break;
+    }
   }
   return check_launch("rmsnorm");
 }

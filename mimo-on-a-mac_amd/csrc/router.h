@@ -14,6 +14,11 @@ struct RouterSmallArgs {
   float* scores;           // [T, E] sigmoid (optional)
   float* keys;             // [T, E] sigmoid + bias (optional)
   uint8_t *xq_hi, *xq_lo, *xq_hs, *xq_ls;   // optional fp8 split of x: [T, H], [T, H/32]
+  // optional RMSNorm of the rows first (the post-attention norm of a decoder layer): logits and split are then of
+  // r = RMSNorm(x) * norm_w, and r itself goes to r_out when given (H a multiple of 256)
+  const uint16_t* norm_w;  // [H] bf16
+  float eps;
+  uint16_t* r_out;         // [T, H] bf16 (optional)
 };
 
 int launch_router_logits_small(const RouterSmallArgs& a, hipStream_t st);   // logits, sigmoid, keys, x split

@@ -8,6 +8,7 @@
 // and permutations are bit-exact against the oracle given identical logits.
 #include "device.h"
 #include "host.h"
+#include "layer.h"
 #include "router.h"
 #include "routing.h"
 
@@ -80,12 +81,40 @@ template <int NCH>
 __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q4 = a.H / 4;
+  const bool norm = a.norm_w != nullptr;
+  __shared__ float wsum[8][4];            // per row, the 4 wave sums of squares (norm only)
   if ((int)blockIdx.x >= a.nlog) {           // hi/lo split of x: one element per lane, 32 lanes per block
-    if (!a.xq_hi) return;
+    if (!a.xq_hi && !a.r_out) return;
     const int64_t n = (int64_t)a.T * a.H;
     const int64_t idx = ((int64_t)(blockIdx.x - a.nlog) * blockDim.x + threadIdx.x);
     const bool live = idx < n;
-    const float v = live ? bf16_to_f32(a.x[idx]) : 0.0f;
+    uint16_t xb = live ? a.x[idx] : (uint16_t)0;
+    if (norm) {
+      // the block's 256 elements lie in one row (H a multiple of 256): that row's inverse RMS, computed exactly as
+      // the logits blocks and the norm kernel compute it
+      const int64_t row = ((int64_t)(blockIdx.x - a.nlog) * blockDim.x) / a.H;
+      const uint16_t wb = a.norm_w[live ? idx - row * a.H : 0];
+      const uint16_t* xq = a.x + row * a.H + wave * q4;
+      uint4 xv[NCH];
+      bool ok[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int off = c * 512 + lane * 8;
+        ok[c] = off < q4;
+        xv[c] = *reinterpret_cast<const uint4*>(xq + (ok[c] ? off : 0));
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) ss = ok[c] ? norm_sq_add8(xv[c], ss) : ss;
+      ss = norm_wave_sum(ss);
+      if (lane == 0) wsum[0][wave] = ss;
+      __syncthreads();
+      xb = norm_apply1(xb, wb, norm_inv(wsum[0], a.H, a.eps));
+      if (live && a.r_out) a.r_out[idx] = xb;
+      if (!a.xq_hi) return;
+    }
+    const float v = live ? bf16_to_f32(xb) : 0.0f;
     float amax = dpp_group_max16(fabsf(v));
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     const int X = fp8_block_exp(amax);
@@ -110,15 +139,15 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
   // 8-element chunks c*512 + lane*8 of that range (c < NCH; chunks past it read element 0 and count 0).
   __shared__ float part[8][4];
   const int e = blockIdx.x;
-  const int q4 = a.H / 4;
   const uint16_t* wrow = a.Wg + (size_t)e * a.H + wave * q4;
-  uint4 wq[NCH], xq[8][NCH];
+  uint4 wq[NCH], xq[8][NCH], nw[NCH];
   bool ok[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int off = c * 512 + lane * 8;
     ok[c] = off < q4;
     wq[c] = *reinterpret_cast<const uint4*>(wrow + (ok[c] ? off : 0));
+    if (norm) nw[c] = *reinterpret_cast<const uint4*>(a.norm_w + wave * q4 + (ok[c] ? off : 0));
   }
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
@@ -128,6 +157,27 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
       if (r < a.T) xq[r][c] = *reinterpret_cast<const uint4*>(xrow + (ok[c] ? c * 512 + lane * 8 : 0));
   }
   __builtin_amdgcn_sched_barrier(0);     // every load is in flight before the arithmetic
+  if (norm) {                            // rows -> r: sums of squares in the norm kernel's order, then r in place
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r < a.T) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) ss = ok[c] ? norm_sq_add8(xq[r][c], ss) : ss;
+        ss = norm_wave_sum(ss);
+        if (lane == 0) wsum[r][wave] = ss;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r < a.T) {
+        const float inv = norm_inv(wsum[r], a.H, a.eps);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) xq[r][c] = norm_apply8(xq[r][c], nw[c], inv);
+      }
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     if (r < a.T) {
@@ -475,7 +525,9 @@ size_t dispatch_workspace(int n, int n_slots) {
 
 int launch_router_logits_small(const RouterSmallArgs& args, hipStream_t st) {
   RouterSmallArgs a = args;
-  int nquant = a.xq_hi ? (int)(((int64_t)a.T * a.H + 255) / 256) : 0;
+  MIMO_REQUIRE(!a.norm_w || (a.H % 256 == 0 && aligned16(a.norm_w) && a.eps >= 0.0f && a.eps == a.eps),
+               MIMO_ERR_ARG, "router: the fused norm needs H a multiple of 256, an aligned weight and eps >= 0");
+  int nquant = (a.xq_hi || (a.norm_w && a.r_out)) ? (int)(((int64_t)a.T * a.H + 255) / 256) : 0;
   a.nlog = a.E;
   const int nch = (a.H / 4 + 511) / 512;
   ProfScope p(st, "router_logits_small");

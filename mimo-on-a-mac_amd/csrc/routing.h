@@ -58,24 +58,15 @@ __device__ __forceinline__ void wave_load_keys(const float* key_row, int E, uint
   for (int j = 0; j < PER; ++j) cv[j] = (lane + 64 * j) < E ? key_to_ordered(kv[j]) + 1u : 0u;
 }
 
-// renorm: divide the selected scores by their sum (model.py:64; mimo_v2.py:190-191 only when norm_topk_prob and
-// k > 1); the weights are then multiplied by scaling (mimo_v2.py:192) unless it is 1.
+// The selected candidates of one row staged in LDS in (j, lane) order, which is ascending id: t_key, t_id, t_sc
+// of lds_sel (positions 0 .. k - 1).
 template <int PER>
-__device__ __forceinline__ void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
-                                                  int32_t* inds_out, float* w_out, int* lds_sel, bool renorm = true) {
+__device__ __forceinline__ void wave_stage_selected(const uint32_t (&cv)[PER], const float (&sc)[PER],
+                                                    const bool (&take)[PER], int* lds_sel) {
   const int lane = threadIdx.x & 63;
   uint32_t* t_key = reinterpret_cast<uint32_t*>(lds_sel);        // [16] selected, in (j, lane) order
   int* t_id = lds_sel + 16;
   float* t_sc = reinterpret_cast<float*>(lds_sel + 32);
-  int* f_id = lds_sel + 48;                                        // [16] in canonical order
-  float* f_sc = reinterpret_cast<float*>(lds_sel + 64);
-  uint32_t cv[PER];
-  float sc[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) sc[j] = s_row[(lane + 64 * j) < E ? lane + 64 * j : 0];   // with the keys below
-  wave_load_keys<PER>(key_row, E, cv);
-  bool take[PER];
-  wave_select_set<PER>(cv, k, take);
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int sel_before = 0;
 #pragma unroll
@@ -89,6 +80,19 @@ __device__ __forceinline__ void wave_select_row_t(const float* s_row, const floa
     }
     sel_before += __popcll(sel);
   }
+}
+
+// Rank the k staged candidates by (key descending, id ascending) and write ids and weights in that order.
+// renorm: divide the selected scores by their sum (model.py:64; mimo_v2.py:190-191 only when norm_topk_prob and
+// k > 1); the weights are then multiplied by scaling (mimo_v2.py:192) unless it is 1.  LDS and registers only.
+__device__ __forceinline__ void wave_rank_renorm(int k, float scaling, int32_t* inds_out, float* w_out, int* lds_sel,
+                                                 bool renorm) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t* t_key = reinterpret_cast<const uint32_t*>(lds_sel);
+  const int* t_id = lds_sel + 16;
+  const float* t_sc = reinterpret_cast<const float*>(lds_sel + 32);
+  int* f_id = lds_sel + 48;                                        // [16] in canonical order
+  float* f_sc = reinterpret_cast<float*>(lds_sel + 64);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -129,6 +133,21 @@ __device__ __forceinline__ void wave_select_row_t(const float* s_row, const floa
     w_out[lane] = wv;
   }
   __builtin_amdgcn_wave_barrier();
+}
+
+template <int PER>
+__device__ __forceinline__ void wave_select_row_t(const float* s_row, const float* key_row, int E, int k, float scaling,
+                                                  int32_t* inds_out, float* w_out, int* lds_sel, bool renorm = true) {
+  const int lane = threadIdx.x & 63;
+  uint32_t cv[PER];
+  float sc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sc[j] = s_row[(lane + 64 * j) < E ? lane + 64 * j : 0];   // with the keys below
+  wave_load_keys<PER>(key_row, E, cv);
+  bool take[PER];
+  wave_select_set<PER>(cv, k, take);
+  wave_stage_selected<PER>(cv, sc, take, lds_sel);
+  wave_rank_renorm(k, scaling, inds_out, w_out, lds_sel, renorm);
 }
 
 __device__ __forceinline__ void wave_select_row(const float* s_row, const float* key_row, int E, int k, float scaling,

@@ -5,9 +5,10 @@ Restated reference behaviour (engine/mimo_stream/model.py:296-340):
     mx.fast.rms_norm: r = w * (x * rsqrt(mean(x^2) + eps)), bf16 in and out, fp32 inside.
   * h = x + y (:340): a bf16 addition.
 
-This build specifies the norm's fp32 arithmetic exactly, so the oracle reproduces the HIP kernel bit for bit:
-  ss  = sum of x^2 in float32 (a bf16 square is exact in float32): 256 partials, partial t adding
-        x[t + 256 j]^2 for j = 0, 1, ... in order; within each group of 64 partials a butterfly
+This build specifies the norm's fp32 arithmetic exactly, so the oracle reproduces the HIP kernels bit for bit:
+  ss  = sum of x^2 in float32 (a bf16 square is exact in float32) as 4 x 64 partials: partial (w, l) adds the
+        squares of the 8-element chunks starting at w H/4 + 512 c + 8 l (c = 0, 1, ...; chunks at or past
+        (w + 1) H/4 are empty) in (chunk, element) order; within each group of 64 partials a butterfly
         (p[l] += p[l ^ s] for s = 32, 16, 8, 4, 2, 1); the 4 group sums as (g0 + g1) + (g2 + g3)
   inv = 1 / sqrt(ss / H + eps)           (float32, each operation correctly rounded)
   r_j = bf16(w_j * bf16(x_j * inv))
@@ -25,16 +26,19 @@ from .mxfp4 import bf16_bits_to_f32, f32_to_bf16_bits
 
 
 def _tree_sum_sq(xf):
-    """The kernel's float32 sum of squares of one row (H = 256 n)."""
+    """The kernels' float32 sum of squares of one row (H = 256 n)."""
     H = xf.shape[-1]
-    n = H // 256
-    sq = (xf * xf).astype(np.float32)                       # exact: bf16 squares fit in float32
-    p = np.zeros(256, np.float32)
-    for j in range(n):                                      # thread t adds its elements in order
-        p = (p + sq[256 * j: 256 * (j + 1)]).astype(np.float32)
-    g = p.reshape(4, 64)
+    q4 = H // 4
+    nch = -(-q4 // 512)
+    sq = np.zeros((4, nch * 512), np.float32)
+    sq[:, :q4] = (xf * xf).astype(np.float32).reshape(4, q4)   # exact: bf16 squares fit in float32
+    ch = sq.reshape(4, nch, 64, 8)                               # [wave, chunk, lane, element]
+    g = np.zeros((4, 64), np.float32)
+    for c in range(nch):                                         # empty chunks add zeros: exact on sums >= 0
+        for j in range(8):
+            g = (g + ch[:, c, :, j]).astype(np.float32)
     idx = np.arange(64)
-    for s in (32, 16, 8, 4, 2, 1):                          # butterfly within each wave
+    for s in (32, 16, 8, 4, 2, 1):                               # butterfly within each wave
         g = (g + g[:, idx ^ s]).astype(np.float32)
     w = g[:, 0]
     return np.float32(np.float32(w[0] + w[1]) + np.float32(w[2] + w[3]))

@@ -36,7 +36,7 @@ def _layer(rng, H, I, E, k, seed):
 
 def test_rmsnorm_and_residual_bit_exact(rng):
     from mimo_stream import _lib
-    for H in (256, 4096):
+    for H in (256, 1024, 2560, 4096, 6144, 8192):    # one to four 8-element chunks per thread, partial chunks
         x = rand_bf16(rng, (7, H)) * np.array([1e-3, 0.1, 1, 1, 3, 50, 1e3], np.float32)[:, None]
         x[1] = 0.0                       # zero row
         x[2] = 1.5                       # constant row
@@ -66,12 +66,12 @@ def test_rmsnorm_rejects_bad_shapes():
         _lib.call("mimo_rmsnorm", _lib.ptr(x), 2, 300, _lib.ptr(w), EPS, _lib.ptr(r), _lib.stream_ptr())
 
 
-@pytest.mark.parametrize("T", [1, 3, 8, 40])
-def test_layer_fused_equals_composition(rng, T):
-    """The layer entry point (norm, block, residual in the combine) == mimo_rmsnorm -> block -> residual add,
-    bit for bit; r and the routes bit-exact against the oracle."""
+@pytest.mark.parametrize("T,shape", [(1, "mimo"), (3, "mimo"), (8, "mimo"), (40, "mimo"), (1, "tiny"), (4, "tiny")])
+def test_layer_fused_equals_composition(rng, T, shape):
+    """The layer entry point (norm inside the router kernel or its own kernel, block, residual in the combine) ==
+    mimo_rmsnorm -> block -> residual add, bit for bit; r and the routes bit-exact against the oracle."""
     from mimo_stream import _lib
-    H, I, E, k = 4096, 2048, 256, 8
+    H, I, E, k = (4096, 2048, 256, 8) if shape == "mimo" else (256, 512, 8, 2)
     layer, bank, W, bias = _layer(rng, H, I, E, k, seed=70 + T)
     x = to_dev_bf16(rand_bf16(rng, (T, H)))
     h, inds, w, r = layer(x, return_routes=True, return_norm=True)

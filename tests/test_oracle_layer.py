@@ -98,3 +98,50 @@ def test_residual_add():
     assert np.all(np.abs(h - exact) <= ulp / 2 + 1e-30)
     np.testing.assert_array_equal(ol.residual_add(x, bits(np.zeros(10000))), x)   # x + 0 = x
     np.testing.assert_array_equal(vals(ol.residual_add(x, bits(-vals(x)))), np.zeros(10000))
+
+
+def _owner_sum_sq(xf):
+    """The same sum from each element's owner (wave, lane, chunk, element), in plain Python float32 steps."""
+    H = xf.shape[-1]
+    q4 = H // 4
+    parts = [[[] for _ in range(64)] for _ in range(4)]
+    for e in range(H):
+        w, off = divmod(e, q4)
+        c, rem = divmod(off, 512)
+        lane, j = divmod(rem, 8)
+        parts[w][lane].append((c, j, np.float32(xf[e]) * np.float32(xf[e])))
+    g = np.zeros((4, 64), np.float32)
+    for w in range(4):
+        for lane in range(64):
+            acc = np.float32(0.0)
+            for _, _, v in sorted(parts[w][lane], key=lambda t: (t[0], t[1])):
+                acc = np.float32(acc + v)
+            g[w, lane] = acc
+    for s in (32, 16, 8, 4, 2, 1):
+        g = np.array([[np.float32(g[w, l] + g[w, l ^ s]) for l in range(64)] for w in range(4)], np.float32)
+    return np.float32(np.float32(g[0, 0] + g[1, 0]) + np.float32(g[2, 0] + g[3, 0]))
+
+
+@pytest.mark.parametrize("H", [256, 2560, 4096])
+def test_tree_sum_order_by_element_owner(H):
+    """The vectorised sum equals the sum taken from each element's owner; rows of mixed magnitudes make the
+    order visible (a thread-strided order gives a different float32 result on some of them)."""
+    rng = np.random.default_rng(H + 1)
+    differs = 0
+    for t in range(6):
+        x = vals(bits(rng.standard_normal(H) * np.exp(rng.uniform(-6, 6, H)))).astype(np.float32)
+        ss = ol._tree_sum_sq(x)
+        assert ss == _owner_sum_sq(x)
+        # the thread-strided order (thread t adding x[t + 256 j]) for contrast
+        sq = (x * x).astype(np.float32)
+        p = np.zeros(256, np.float32)
+        for j in range(H // 256):
+            p = (p + sq[256 * j: 256 * (j + 1)]).astype(np.float32)
+        g = p.reshape(4, 64)
+        idx = np.arange(64)
+        for s in (32, 16, 8, 4, 2, 1):
+            g = (g + g[:, idx ^ s]).astype(np.float32)
+        strided = np.float32(np.float32(g[0, 0] + g[1, 0]) + np.float32(g[2, 0] + g[3, 0]))
+        differs += int(strided != ss)
+    if H > 256:
+        assert differs > 0
