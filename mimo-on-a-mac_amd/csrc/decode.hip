@@ -252,11 +252,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
     const int proj = p >> (5 + lg_pr), row = (p >> lg_pr) & 31, c = p & ((1 << lg_pr) - 1);
     return reinterpret_cast<uint2*>(lds + (proj * 32 + row) * L.RS + 8 * c);
   };
+  // the scale pieces, then the weight batch: the activation rows and the scales land first, so each MFMA step
+  // can start as soon as its own weights arrive
+  const uint2 sp0 = *piece_src(q0);
+  const uint2 sp1 = *piece_src(q1);
   uint4 bg[NS], bu[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) { bg[s] = gw[4 * s]; bu[s] = upw[4 * s]; }
-  const uint2 sp0 = *piece_src(q0);
-  const uint2 sp1 = *piece_src(q1);
   __builtin_amdgcn_sched_barrier(0);
   if (ROUTED && fast && publisher && wave == 0) {
     // the step's full routing for the down kernel while this block's loads stream: ranking, renormalisation and
@@ -269,9 +271,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
                       &g_nu[0], &g_nu[1], lurows, luw);
   }
   __builtin_amdgcn_sched_barrier(0);
+  wait_vm_keep<2 * NS>();    // everything before the weight batch has landed: staged rows and scale pieces
   if (p0 < npieces) *piece_dst(p0) = sp0;
   if (p1 < npieces) *piece_dst(p1) = sp1;
-  wait_vm_all();
   __syncthreads();
 
   v4f accg = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -475,8 +477,9 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
 #pragma unroll
     for (int s = 0; s < NS; ++s) bw[s] = dw[4 * s];
     __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before anything waits
+    wait_vm_keep<NS>();                  // the staged rows and the scales have landed; each MFMA step then waits
+                                         // only for its own weights
     if (lane < 16 * LPR) *reinterpret_cast<uint2*>(&wsc[wave][srow * SRS + 2 * spart]) = sraw;
-    wait_vm_all();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");

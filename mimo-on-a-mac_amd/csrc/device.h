@@ -290,6 +290,13 @@ __device__ __forceinline__ void gload16(v4i& dst, const void* gbase, uint32_t vo
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every global load of the wave has landed,
 // including the global -> LDS copies above
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N): at most the N most recent vector memory loads still in flight (loads, including the LDS
+// copies above, complete in issue order, so everything issued before them has landed)
+template <int N>
+__device__ __forceinline__ void wait_vm_keep() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
 
 // ------------------------------------------------------------------ misc
 __device__ __forceinline__ uint32_t load_u8x4(const uint8_t* p) { return *(const uint32_t*)p; }
