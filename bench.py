@@ -464,7 +464,8 @@ def mfma_parse(pmc_dir, trace_dir):
 
 def layer_case(layers, T, steps, warmup, seed, device):
     """The MoE half of a decoder layer (post-attention RMSNorm, block, residual added in the combine) against the
-    block alone on the same rows, layers rotated; the difference is what the norm and the residual cost."""
+    block alone on the normalised rows (so both route identically), layers rotated; the difference is what the
+    norm and the residual cost."""
     import numpy as np
     import torch
     from mimo_stream import MoELayer
@@ -480,8 +481,9 @@ def layer_case(layers, T, steps, warmup, seed, device):
     lays = [MoELayer(b, (1.0 + 0.1 * torch.randn(H, device=device, generator=g)).to(torch.bfloat16), 1e-5)
             for b in layers.blocks]
     blocks = layers.blocks
+    Rd = {(j, i): lays[j].norm(Xd[i]) for j in range(n) for i in range(nin)}
     ms_l = time_graph(lambda s: lays[s % n](Xd[s % nin]), steps, warmup)
-    ms_b = time_graph(lambda s: blocks[s % n](Xd[s % nin]), steps, warmup)
+    ms_b = time_graph(lambda s: blocks[s % n](Rd[(s % n, s % nin)]), steps, warmup)
     return {"rows": T, "layer_us": ms_l * 1e3, "block_us": ms_b * 1e3, "norm_and_residual_us": (ms_l - ms_b) * 1e3}
 
 
