@@ -167,7 +167,8 @@ __device__ __forceinline__ void publish_routes(const ExpertsArgs& a, const int32
   if (tid == 0) { a.rt_nu[0] = g_nu[0]; a.rt_status[0] = g_nu[1]; }
 }
 
-template <int NS, bool ROUTED>
+// FAST2 (routed only; the launcher checks its conditions): two rows with expert ids as slots
+template <int NS, bool ROUTED, bool FAST2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a, int rl) {
   extern __shared__ __align__(16) uint8_t lds[];
   // routed grouping (ROUTED only): kept for the publication at the end of block (0, 0)
@@ -183,26 +184,56 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar registers)
   int U, cnt_raw, slot, tok;          // tok: lane c < R holds the token of the expert's row c
-  // one row with expert ids as slots: a block needs only its expert, the u-th selected one in ascending id order
-  const bool fast = ROUTED && a.M == 1 && a.slot_of == nullptr && a.S >= a.E;
+  // one or two rows with expert ids as slots: a block needs only its expert, the u-th distinct selected id in
+  // ascending order, and which rows chose it; the ranking and grouping are left to the publishing block
+  const bool fast = ROUTED && (FAST2 || (a.M == 1 && a.slot_of == nullptr && a.S >= a.E));
   const bool publisher = ROUTED && blockIdx.x == 0 && blockIdx.y == 0;
+  __shared__ uint64_t fast_mask[FAST2 ? 2 : 1][4];   // per row, the selection as ballot words (bit lane of word j)
   if (ROUTED && fast) {
-    if (wave == 0) {
+    if (wave < (FAST2 ? 2 : 1)) {
       uint32_t cv[4];
       float sc[4];
       bool take[4];
+      const int rb = wave * a.E;
 #pragma unroll
       for (int j = 0; j < 4; ++j)                       // the scores only for the block that publishes the routes
-        sc[j] = publisher ? a.scores[(lane + 64 * j) < a.E ? lane + 64 * j : 0] : 0.0f;
-      wave_load_keys<4>(a.keys, a.E, cv);              // E <= 256 on this path
+        sc[j] = publisher ? a.scores[rb + ((lane + 64 * j) < a.E ? lane + 64 * j : 0)] : 0.0f;
+      wave_load_keys<4>(a.keys + rb, a.E, cv);         // E <= 256 on this path
       wave_select_set<4>(cv, a.k, take);
-      wave_stage_selected<4>(cv, sc, take, sel[0]);     // ids in ascending order at sel[0][16 ..]
+      wave_stage_selected<4>(cv, sc, take, sel[wave]);  // ids in ascending order at sel[wave][16 ..]
+      if constexpr (FAST2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint64_t m = __ballot(take[j]);
+          if (lane == 0) fast_mask[wave][j] = m;
+        }
+      }
     }
     __syncthreads();
-    U = a.k;                                            // distinct experts, one row each
-    cnt_raw = 1;
-    slot = u < U ? sel[0][16 + u] : 0;
-    tok = 0;
+    if constexpr (!FAST2) {
+      U = a.k;                                          // distinct experts, one row each
+      cnt_raw = 1;
+      slot = u < U ? sel[0][16 + u] : 0;
+      tok = 0;
+    } else {
+      // distinct experts of the step in ascending id: the union of the two rows' selections
+      uint64_t mu[4];
+      int before = 0, jsel = 0, nsel = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        mu[j] = fast_mask[0][j] | fast_mask[1][j];
+        const int c = __popcll(mu[j]);
+        if (u >= before && u < before + c) { jsel = j; nsel = u - before; }
+        before += c;
+      }
+      U = before;
+      const int bit = u < U ? nth_set_bit(mu[jsel], nsel) : 0;
+      slot = 64 * jsel + bit;
+      const int in0 = (int)((fast_mask[0][jsel] >> bit) & 1ull);
+      const int in1 = (int)((fast_mask[1][jsel] >> bit) & 1ull);
+      cnt_raw = in0 + in1;
+      tok = (lane == 0 && in0) ? 0 : 1;                 // the expert's first row: row 0 if it chose it, else row 1
+    }
   } else if (ROUTED) {
     // routes of this step: wave r selects row r (top-k and renormalisation), wave 0 groups them by slot; every
     // block does this (it costs less than a separate launch) and block (0, 0) publishes the result at its end
@@ -262,12 +293,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   __builtin_amdgcn_sched_barrier(0);
   if (ROUTED && fast && publisher && wave == 0) {
     // the step's full routing for the down kernel while this block's loads stream: ranking, renormalisation and
-    // grouping of the staged selection touch only LDS and registers (workgroup fences wait on LDS only)
-    wave_rank_renorm(a.k, 1.0f, s_inds, s_w, sel[0], true);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    wave_group_routes(s_inds, s_w, nullptr, 1, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
+    // grouping of the staged selections touch only LDS and registers (workgroup fences wait on LDS only)
+    for (int r = 0; r < a.M; ++r) {
+      wave_rank_renorm(a.k, 1.0f, s_inds + r * a.k, s_w + r * a.k, sel[r], true);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
+    wave_group_routes(s_inds, s_w, nullptr, a.M, a.k, a.R, a.S, a.Umax, g_uids, g_urows, g_ucnt, g_uw, g_gidx,
                       &g_nu[0], &g_nu[1], lurows, luw);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -627,13 +660,13 @@ static int allow_lds(const void* fn, size_t bytes, int* allowed) {
   return MIMO_OK;
 }
 
-template <int NS, bool ROUTED>
+template <int NS, bool ROUTED, bool FAST2>
 static int launch_gateup(const ExpertsArgs& a, int rl, hipStream_t st) {
   static int allowed = 0;
   const size_t lds = (size_t)gateup_lds(a.H, rl).total;
-  int rc = allow_lds(reinterpret_cast<const void*>(&decode_gateup_kernel<NS, ROUTED>), lds, &allowed);
+  int rc = allow_lds(reinterpret_cast<const void*>(&decode_gateup_kernel<NS, ROUTED, FAST2>), lds, &allowed);
   if (rc) return rc;
-  decode_gateup_kernel<NS, ROUTED><<<dim3(a.I / 32, a.Umax), 512, lds, st>>>(a, rl);
+  decode_gateup_kernel<NS, ROUTED, FAST2><<<dim3(a.I / 32, a.Umax), 512, lds, st>>>(a, rl);
   return MIMO_OK;
 }
 
@@ -664,19 +697,26 @@ static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream
   int rc;
   {
     ProfScope p(st, "decode_gateup");
+    // two rows with expert ids as slots (E <= 256 for a fused selection): each block finds its own expert from
+    // the two threshold searches alone (one row does the same inside the general routed kernel)
+    const bool fast2 = fused_select && a.slot_of == nullptr && a.S >= a.E && M == 2;
     if (fused_select) {   // cheaper than a separate selection launch
-      switch (ns) {
-        case 8: rc = launch_gateup<8, true>(a, rl, st); break;
-        case 4: rc = launch_gateup<4, true>(a, rl, st); break;
-        case 2: rc = launch_gateup<2, true>(a, rl, st); break;
-        default: rc = launch_gateup<1, true>(a, rl, st); break;
+      switch (ns * 2 + (fast2 ? 1 : 0)) {
+        case 17: rc = launch_gateup<8, true, true>(a, rl, st); break;
+        case 16: rc = launch_gateup<8, true, false>(a, rl, st); break;
+        case 9: rc = launch_gateup<4, true, true>(a, rl, st); break;
+        case 8: rc = launch_gateup<4, true, false>(a, rl, st); break;
+        case 5: rc = launch_gateup<2, true, true>(a, rl, st); break;
+        case 4: rc = launch_gateup<2, true, false>(a, rl, st); break;
+        case 3: rc = launch_gateup<1, true, true>(a, rl, st); break;
+        default: rc = launch_gateup<1, true, false>(a, rl, st); break;
       }
     } else {
       switch (ns) {
-        case 8: rc = launch_gateup<8, false>(a, rl, st); break;
-        case 4: rc = launch_gateup<4, false>(a, rl, st); break;
-        case 2: rc = launch_gateup<2, false>(a, rl, st); break;
-        default: rc = launch_gateup<1, false>(a, rl, st); break;
+        case 8: rc = launch_gateup<8, false, false>(a, rl, st); break;
+        case 4: rc = launch_gateup<4, false, false>(a, rl, st); break;
+        case 2: rc = launch_gateup<2, false, false>(a, rl, st); break;
+        default: rc = launch_gateup<1, false, false>(a, rl, st); break;
       }
     }
   }

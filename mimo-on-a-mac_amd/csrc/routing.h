@@ -48,6 +48,24 @@ __device__ __forceinline__ void wave_select_set(const uint32_t (&cv)[PER], int k
   }
 }
 
+// position of the n-th (0-based) set bit of m, n < popcount(m): a binary search on the halves' popcounts
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int n) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const uint64_t low = m & ((1ull << w) - 1ull);
+    const int c = __popcll(low);
+    if (n >= c) {
+      n -= c;
+      m >>= w;
+      pos += w;
+    } else {
+      m = low;
+    }
+  }
+  return pos;
+}
+
 template <int PER>
 __device__ __forceinline__ void wave_load_keys(const float* key_row, int E, uint32_t (&cv)[PER]) {
   const int lane = threadIdx.x & 63;
