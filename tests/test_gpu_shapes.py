@@ -41,7 +41,7 @@ def _block(rng, H, I, E, k, seed):
 def test_decode_block_shapes(rng, H, I, E, k):
     blk, bank, W, bias = _block(rng, H, I, E, k, seed=H + I + E)
     pool = pool_np(bank)
-    for M in (1, 3, 8):
+    for M in (1, 2, 3, 8):
         x = rand_bf16(rng, (M, H))
         y, inds, w = blk(to_dev_bf16(x), return_routes=True)
         gi, gw = inds.cpu().numpy(), w.cpu().numpy()
@@ -74,3 +74,29 @@ def test_prefill_block_shapes(rng, H, I, E, k):
         y = blk._moe_prefill(to_dev_bf16(x), torch.from_numpy(inds).cuda(), torch.from_numpy(w).cuda())
         oy = ox.moe_prefill(x, pool, inds, w)
         assert_bf16_close(bf16_np(y), oy, what=f"prefill H={H} I={I} E={E} k={k} T={T}")
+
+
+def test_two_row_decode_shared_experts(rng):
+    """Two rows with identity slots take the path where every block finds its expert from the union of the two
+    rows' selections: identical rows (every expert on both rows), nearby rows (partial overlap) and unrelated
+    rows, at the MiMo shape (256 experts: all four ballot words)."""
+    H, I, E, k = 4096, 2048, 256, 8
+    blk, bank, W, bias = _block(rng, H, I, E, k, seed=2024)
+    pool = pool_np(bank)
+    base = rand_bf16(rng, (1, H))
+    cases = {"identical": np.concatenate([base, base]),
+             "nearby": np.concatenate([base, base + rand_bf16(rng, (1, H), 0.3)]),
+             "unrelated": rand_bf16(rng, (2, H))}
+    for name, x in cases.items():
+        x = to_dev_bf16(x).float().cpu().numpy()          # bf16-exact rows
+        y, inds, w = blk(to_dev_bf16(x), return_routes=True)
+        gi, gw = inds.cpu().numpy(), w.cpu().numpy()
+        logits, _, _ = blk.router.logits_and_routes(to_dev_bf16(x))
+        oi, ow = orr.select_topk(logits.cpu().numpy(), bias, k)
+        np.testing.assert_array_equal(gi, oi)
+        np.testing.assert_array_equal(gw, ow)
+        uids, urows, ucnt, uw, gidx = orr.group_routes(gi, gw, R=8)
+        if name == "identical":
+            assert len(uids) == k and (ucnt[:k] == 2).all()
+        oy, _, _ = ox.moe_experts(x, pool, uids, urows, ucnt, uw, gidx, k, R=8)
+        assert_bf16_close(bf16_np(y), oy, what=f"two-row decode, {name} rows")
