@@ -160,3 +160,20 @@ def test_decode_vs_prefill_through_a_layer_stack(rng):
         hd.append(h)
     hd = torch.cat(hd)
     assert_bf16_close(hd.float().cpu().numpy(), hp.float().cpu().numpy(), what="decode vs prefill, 3 layers")
+
+
+@pytest.mark.parametrize("H,I,E,k", [(512, 1024, 16, 3), (1024, 512, 32, 4), (2048, 1024, 64, 6)])
+def test_layer_decode_other_hidden_sizes(rng, H, I, E, k):
+    """The router kernel's own norm at hidden sizes where a wave holds partial chunk sets (H / 4 < 512): the
+    layer step equals mimo_rmsnorm -> block -> residual add bit for bit, and r equals the oracle's norm."""
+    from mimo_stream import _lib
+    layer, bank, W, bias = _layer(rng, H, I, E, k, seed=H + E)
+    for T in (1, 2, 5):
+        x = to_dev_bf16(rand_bf16(rng, (T, H)))
+        h, inds, w, r = layer(x, return_routes=True, return_norm=True)
+        np.testing.assert_array_equal(bf16_bits(r), ol.rmsnorm(bf16_bits(x), bf16_bits(layer.norm_weight), EPS))
+        y, inds2, w2 = layer.block(layer.norm(x), return_routes=True)
+        assert torch.equal(inds, inds2) and torch.equal(w, w2)
+        h2 = torch.empty_like(x)
+        _lib.call("mimo_residual_add", _lib.ptr(x), _lib.ptr(y), x.numel(), _lib.ptr(h2), _lib.stream_ptr())
+        assert torch.equal(h, h2), (H, T)
