@@ -64,6 +64,12 @@ def test_rmsnorm_rejects_bad_shapes():
     r = torch.empty_like(x)
     with pytest.raises(ValueError):
         _lib.call("mimo_rmsnorm", _lib.ptr(x), 2, 300, _lib.ptr(w), EPS, _lib.ptr(r), _lib.stream_ptr())
+    # the kernel reads 16-byte chunks: rows that are not 16-byte aligned are refused before any launch
+    xf = torch.zeros(2 * 256 + 8, dtype=torch.bfloat16, device="cuda")
+    w2 = torch.ones(256, dtype=torch.bfloat16, device="cuda")
+    r2 = torch.empty(2, 256, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        _lib.call("mimo_rmsnorm", _lib.ptr(xf[1:]), 2, 256, _lib.ptr(w2), EPS, _lib.ptr(r2), _lib.stream_ptr())
 
 
 @pytest.mark.parametrize("T,shape", [(1, "mimo"), (3, "mimo"), (8, "mimo"), (40, "mimo"), (1, "tiny"), (4, "tiny")])
