@@ -15,6 +15,15 @@
  * Workspaces: entry points that take (ws, ws_bytes) need a caller-owned device buffer of at least the size
  * the matching *_workspace_size() returns; its contents need no initialisation (every kernel writes what it
  * later reads).  Calls that share one workspace must be ordered on one stream.
+ *
+ * Device status: the fused entry points (mimo_moe_decode, mimo_moe_prefill, mimo_moe_prefill_block,
+ * mimo_moe_layer_decode, mimo_moe_layer_prefill) take an optional status_out, a device int32 [1] that the
+ * call's own kernels overwrite with MIMO_OK or the failure they found: MIMO_ERR_SLOT when a selected
+ * expert has no resident slot (slot_of entry outside [0, n_slots)) and MIMO_ERR_ROWS_PER_EXPERT when more
+ * than 8 rows reach one slot (kernels.py:167-168).  Such a route is computed with slot 0 instead of being
+ * read out of bounds, so the outputs of a call whose status is not MIMO_OK are not valid.  The word is
+ * written on the stream like every output (read it after the stream's work, no host sync inside the call);
+ * NULL keeps it in the workspace.
  */
 #ifndef MIMO_MOE_H
 #define MIMO_MOE_H
@@ -26,7 +35,7 @@
 extern "C" {
 #endif
 
-#define MIMO_ABI_VERSION 1
+#define MIMO_ABI_VERSION 2
 
 enum {
   MIMO_OK = 0,
@@ -138,23 +147,27 @@ size_t mimo_moe_experts_workspace_size(int M, int Umax, int R, int H, int I);
 /* One MoE block in decode (model.py:303-325 with _moe_small :184-219, every expert resident):
  * router -> grouping -> experts -> combine for M <= 8 rows, no host synchronisation.  M == 1 uses the
  * gather_qmm rounding (bf16 expert outputs, model.py:173-182), M >= 2 the distinct-expert kernels' fp32
- * partials (kernels.py:120).  inds_out / w_out (optional) receive the routes. */
+ * partials (kernels.py:120).  inds_out / w_out (optional) receive the routes, status_out (optional) the
+ * device status. */
 int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
                     int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
-                    void* ws, size_t ws_bytes, void* stream);
+                    int32_t* status_out, void* ws, size_t ws_bytes, void* stream);
 size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I);
 
 /* _moe_prefill (model.py:230-271) with every expert resident: slot_inds int32 [T, k] (slots), w fp32
  * [T, k]; sorted-by-slot grouped GEMMs on block-scaled MFMA, bf16 expert outputs, fixed-order weighted
- * combine.  y bf16 [T, H]. */
+ * combine.  y bf16 [T, H]; status_out (optional): MIMO_ERR_SLOT when a slot id is outside [0, n_slots). */
 int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* w, int k,
-                     const mimo_bank* bank, uint16_t* y, void* ws, size_t ws_bytes, void* stream);
+                     const mimo_bank* bank, uint16_t* y, int32_t* status_out, void* ws, size_t ws_bytes,
+                     void* stream);
 size_t mimo_moe_prefill_workspace_size(int T, int k, int n_slots, int H, int I);
 
-/* Router + _moe_prefill for one chunk (model.py:303, :335-336): y bf16 [T, H]; inds_out / w_out optional. */
+/* Router + _moe_prefill for one chunk (model.py:303, :335-336): y bf16 [T, H]; inds_out / w_out / status_out
+ * optional. */
 int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const float* bias,
                            const int32_t* slot_of, int E, int k, const mimo_bank* bank, uint16_t* y,
-                           int32_t* inds_out, float* w_out, void* ws, size_t ws_bytes, void* stream);
+                           int32_t* inds_out, float* w_out, int32_t* status_out, void* ws, size_t ws_bytes,
+                           void* stream);
 size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, int H, int I);
 
 /* ---------------------------------------------------------------- the decoder layer around the block */
@@ -171,19 +184,19 @@ int mimo_residual_add(const uint16_t* x, const uint16_t* y, int64_t n, uint16_t*
 /* The MoE half of a decoder layer in decode (model.py:299-340 for T <= 8): r = RMSNorm(x) * norm_w (computed
  * inside the router kernel, bit-identical to mimo_rmsnorm), the decode block on r (as mimo_moe_decode),
  * h = bf16(x + y) in the block's combine.  h may alias x; r_out (optional, not aliasing x or h) receives r;
- * inds_out / w_out (optional) the routes. */
+ * inds_out / w_out (optional) the routes, status_out (optional) the device status. */
 int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
                           const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank,
-                          uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws,
-                          size_t ws_bytes, void* stream);
+                          uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out, int32_t* status_out,
+                          void* ws, size_t ws_bytes, void* stream);
 size_t mimo_moe_layer_decode_workspace_size(int M, int E, int k, int H, int I);
 
 /* The same for a prefill chunk (model.py:299-340 for T > 8): RMSNorm, the prefill block on r (as
  * mimo_moe_prefill_block), h = bf16(x + y) in the combine.  h may alias x. */
 int mimo_moe_layer_prefill(const uint16_t* x, int T, const uint16_t* norm_w, float eps, const uint16_t* Wg,
                            const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank,
-                           uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws,
-                           size_t ws_bytes, void* stream);
+                           uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out, int32_t* status_out,
+                           void* ws, size_t ws_bytes, void* stream);
 size_t mimo_moe_layer_prefill_workspace_size(int T, int E, int k, int n_slots, int H, int I);
 
 /* ---------------------------------------------------------------- measurement */

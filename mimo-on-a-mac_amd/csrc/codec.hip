@@ -64,7 +64,10 @@ void prof_begin(hipStream_t st, const char* name) {
   }
   hipEvent_t e = prof_event();
   if (!e) return;
-  hipEventRecord(e, st);
+  if (hipEventRecord(e, st) != hipSuccess) {   // timing is best effort: this launch goes unrecorded
+    g_prof_pool.push_back(e);
+    return;
+  }
   g_prof_open = name;
   g_prof_open_ev = e;
   g_prof_open_owns = true;
@@ -75,8 +78,13 @@ void prof_end(hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
   if (!g_prof_open) return;
   hipEvent_t e = prof_event();
-  if (!e) return;
-  hipEventRecord(e, st);
+  if (!e || hipEventRecord(e, st) != hipSuccess) {   // drop this launch's record; the chain restarts
+    if (e) g_prof_pool.push_back(e);
+    if (g_prof_open_owns) g_prof_pool.push_back(g_prof_open_ev);
+    g_prof_open = nullptr;
+    g_prof_last_end = nullptr;
+    return;
+  }
   g_prof.push_back({g_prof_open, g_prof_open_ev, e, g_prof_open_owns});
   g_prof_open = nullptr;
   g_prof_last_end = e;

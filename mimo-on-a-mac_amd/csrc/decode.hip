@@ -801,7 +801,9 @@ static const int kDecodeR = 8;   // VERIFY_MAX (model.py:27): rows per distinct 
 
 size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
   Carve c(nullptr, 0);
-  int Umax = M * k < E ? M * k : E;
+  // the call carves min(M * k, n_slots) distinct-expert entries; the bank's slot count is not an argument here,
+  // so size for M * k, which covers every bank
+  const int Umax = M * k;
   float *l, *s, *kk, *w, *uw;
   int32_t *inds, *uids, *urows, *ucnt, *nu, *st;
   uint32_t* gidx;
@@ -817,8 +819,8 @@ namespace mimo {
 // stream added in the combine; norm_w: optional RMSNorm of the rows inside the router kernel (r to r_out if given).
 static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
                        int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
-                       const uint16_t* resid, const uint16_t* norm_w, float eps, uint16_t* r_out, void* ws,
-                       size_t ws_bytes, hipStream_t st) {
+                       const uint16_t* resid, const uint16_t* norm_w, float eps, uint16_t* r_out,
+                       int32_t* status_out, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = check_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_decode: null pointer");
@@ -857,7 +859,7 @@ static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float
   a.inds_out = inds_out ? inds_out : inds;
   a.w_out = w_out ? w_out : w;
   a.rt_uids = uids; a.rt_urows = urows; a.rt_ucnt = ucnt; a.rt_uw = uw; a.rt_gidx = gidx; a.rt_nu = nu;
-  a.rt_status = status;
+  a.rt_status = status_out ? status_out : status;   // written on every call (block (0, 0) or the selection launch)
   a.resid = resid;
   // M == 1 follows _gather_m1 (bf16 expert outputs, model.py:173-182); M >= 2 the distinct-expert kernels
   return run_experts(a, M, M == 1 ? 1 : 0, st);
@@ -867,11 +869,11 @@ static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float
 extern "C" {
 
 int mimo_moe_decode(const uint16_t* x, int M, const uint16_t* Wg, const float* bias, const int32_t* slot_of, int E,
-                    int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
-                    size_t ws_bytes, void* stream) {
+                    int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, int32_t* status_out,
+                    void* ws, size_t ws_bytes, void* stream) {
   ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
-  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, nullptr, 0.0f, nullptr, ws,
-                     ws_bytes, as_stream(stream));
+  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, nullptr, 0.0f, nullptr,
+                     status_out, ws, ws_bytes, as_stream(stream));
 }
 
 // The layer step normalises the rows inside the router kernel: no rows of r are kept unless r_out asks for them,
@@ -882,7 +884,8 @@ size_t mimo_moe_layer_decode_workspace_size(int M, int E, int k, int H, int I) {
 
 int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
                           const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank, uint16_t* h,
-                          uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws, size_t ws_bytes, void* stream) {
+                          uint16_t* r_out, int32_t* inds_out, float* w_out, int32_t* status_out, void* ws,
+                          size_t ws_bytes, void* stream) {
   ProfChain chain;
   MIMO_REQUIRE(x && norm_w && h && bank, MIMO_ERR_ARG, "moe_layer_decode: null pointer");
   MIMO_REQUIRE(M >= 1 && M <= 8, MIMO_ERR_SHAPE, "moe_layer_decode: need 1 <= M <= 8");
@@ -890,8 +893,8 @@ int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, floa
                "moe_layer_decode: 16-byte alignment");
   MIMO_REQUIRE(r_out != x && r_out != h, MIMO_ERR_ARG, "moe_layer_decode: r_out may not alias x or h");
   MIMO_REQUIRE(eps >= 0.0f && eps == eps, MIMO_ERR_ARG, "moe_layer_decode: eps must be a non-negative number");
-  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x, norm_w, eps, r_out, ws, ws_bytes,
-                     as_stream(stream));
+  return decode_impl(x, M, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x, norm_w, eps, r_out, status_out, ws,
+                     ws_bytes, as_stream(stream));
 }
 
 }  // extern "C"

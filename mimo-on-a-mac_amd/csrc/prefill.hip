@@ -555,7 +555,7 @@ size_t mimo_moe_prefill_workspace_size(int T, int k, int n_slots, int H, int I) 
 }
 
 int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* w, int k, const mimo_bank* bank,
-                     uint16_t* y, void* ws, size_t ws_bytes, void* stream) {
+                     uint16_t* y, int32_t* status_out, void* ws, size_t ws_bytes, void* stream) {
   ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
   int rc = check_prefill_bank(bank);
   if (rc) return rc;
@@ -565,6 +565,7 @@ int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const f
   Carve c(ws, ws_bytes);
   PrefillWs pw = carve_prefill(c, T, k, bank->n_slots, bank->hidden, bank->inter, 0);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill: workspace too small (need %zu)", c.off);
+  if (status_out) pw.status = status_out;
   reset_status_kernel<<<1, 1, 0, as_stream(stream)>>>(pw.status);
   return run_prefill(x, T, slot_inds, w, k, bank, y, pw, as_stream(stream));
 }
@@ -581,7 +582,7 @@ namespace mimo {
 // Router + grouped GEMMs + combine on rows x; resid: optional residual stream added in the combine.
 static int prefill_block_impl(const uint16_t* x, int T, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
                               int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
-                              const uint16_t* resid, void* ws, size_t ws_bytes, hipStream_t st) {
+                              const uint16_t* resid, int32_t* status_out, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = check_prefill_bank(bank);
   if (rc) return rc;
   MIMO_REQUIRE(x && Wg && bias && y, MIMO_ERR_ARG, "moe_prefill_block: null pointer");
@@ -593,6 +594,7 @@ static int prefill_block_impl(const uint16_t* x, int T, const uint16_t* Wg, cons
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill_block: workspace too small (need %zu)", c.off);
   int32_t* inds = inds_out ? inds_out : pw.inds;
   float* wts = w_out ? w_out : pw.w;
+  if (status_out) pw.status = status_out;
   reset_status_kernel<<<1, 1, 0, st>>>(pw.status);
   rc = launch_router_logits(x, Wg, T, bank->hidden, E, pw.logits, st);
   if (rc) return rc;
@@ -606,10 +608,10 @@ static int prefill_block_impl(const uint16_t* x, int T, const uint16_t* Wg, cons
 extern "C" {
 
 int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const float* bias, const int32_t* slot_of,
-                           int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out, void* ws,
-                           size_t ws_bytes, void* stream) {
+                           int E, int k, const mimo_bank* bank, uint16_t* y, int32_t* inds_out, float* w_out,
+                           int32_t* status_out, void* ws, size_t ws_bytes, void* stream) {
   ProfChain chain;   // per-kernel timing (when enabled) back to back within this call
-  return prefill_block_impl(x, T, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, ws, ws_bytes,
+  return prefill_block_impl(x, T, Wg, bias, slot_of, E, k, bank, y, inds_out, w_out, nullptr, status_out, ws, ws_bytes,
                             as_stream(stream));
 }
 
@@ -622,7 +624,8 @@ size_t mimo_moe_layer_prefill_workspace_size(int T, int E, int k, int n_slots, i
 
 int mimo_moe_layer_prefill(const uint16_t* x, int T, const uint16_t* norm_w, float eps, const uint16_t* Wg,
                            const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank, uint16_t* h,
-                           uint16_t* r_out, int32_t* inds_out, float* w_out, void* ws, size_t ws_bytes, void* stream) {
+                           uint16_t* r_out, int32_t* inds_out, float* w_out, int32_t* status_out, void* ws,
+                           size_t ws_bytes, void* stream) {
   ProfChain chain;
   MIMO_REQUIRE(x && norm_w && h && bank, MIMO_ERR_ARG, "moe_layer_prefill: null pointer");
   MIMO_REQUIRE(T >= 1, MIMO_ERR_SHAPE, "moe_layer_prefill: need T >= 1");
@@ -637,7 +640,7 @@ int mimo_moe_layer_prefill(const uint16_t* x, int T, const uint16_t* norm_w, flo
   uint16_t* r = r_out ? r_out : static_cast<uint16_t*>(ws);
   int rc = launch_rmsnorm(x, T, H, norm_w, eps, r, st);
   if (rc) return rc;
-  return prefill_block_impl(r, T, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x,
+  return prefill_block_impl(r, T, Wg, bias, slot_of, E, k, bank, h, inds_out, w_out, x, status_out,
                             static_cast<uint8_t*>(ws) + rb, ws_bytes - rb, st);
 }
 

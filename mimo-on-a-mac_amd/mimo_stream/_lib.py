@@ -9,7 +9,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmimo_moe.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MIMO_OK = 0
 ERR_SHAPE, ERR_ALIGN, ERR_ROWS_PER_EXPERT, ERR_SLOT, ERR_WORKSPACE, ERR_HIP, ERR_ARG = -1, -2, -3, -4, -5, -6, -7
@@ -49,17 +49,17 @@ SIGNATURES = {
     "mimo_prefill_dispatch_workspace_size": (SZ, [I32, I32, I32]),
     "mimo_moe_experts": (I32, [P, I32, BANKP, P, P, P, P, P, I32, I32, P, I32, I32, P, P, P, P, SZ, P]),
     "mimo_moe_experts_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
-    "mimo_moe_decode": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, SZ, P]),
+    "mimo_moe_decode": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
     "mimo_moe_decode_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
-    "mimo_moe_prefill": (I32, [P, I32, P, P, I32, BANKP, P, P, SZ, P]),
+    "mimo_moe_prefill": (I32, [P, I32, P, P, I32, BANKP, P, P, P, SZ, P]),
     "mimo_moe_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
-    "mimo_moe_prefill_block": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, SZ, P]),
+    "mimo_moe_prefill_block": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
     "mimo_moe_prefill_block_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "mimo_rmsnorm": (I32, [P, I32, I32, P, F32, P, P]),
     "mimo_residual_add": (I32, [P, P, I64, P, P]),
-    "mimo_moe_layer_decode": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
+    "mimo_moe_layer_decode": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, P, SZ, P]),
     "mimo_moe_layer_decode_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
-    "mimo_moe_layer_prefill": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
+    "mimo_moe_layer_prefill": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, P, SZ, P]),
     "mimo_moe_layer_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "mimo_profile_enable": (I32, [I32]),
     "mimo_profile_read": (I32, [I32, P, P, P]),
@@ -101,6 +101,18 @@ def call(name, *args):
     check(getattr(load(), name)(*args), name)
 
 
+STATUS_MESSAGES = {ERR_SLOT: "a selected expert has no resident slot (slot_of entry outside the bank)",
+                   ERR_ROWS_PER_EXPERT: "more than 8 rows routed to one slot"}
+
+
+def check_status(status, what=""):
+    """Raise ValueError if a device status word (int32 tensor, written by a fused entry point on the current
+    stream) holds an error code.  Synchronises with the stream that wrote it."""
+    code = int(status.reshape(-1)[0].item())
+    if code != MIMO_OK:
+        raise ValueError(f"{what}: {STATUS_MESSAGES.get(code, 'device error')} (code {code})")
+
+
 def ptr(t):
     """Device pointer of a tensor (None -> NULL)."""
     return None if t is None else ctypes.c_void_p(t.data_ptr())
@@ -120,10 +132,10 @@ _ws = {}
 
 
 def workspace(nbytes, device, tag):
-    """Zeroed device workspace of at least nbytes, cached per (device, stream, entry point tag).
+    """Device workspace of at least nbytes, cached per (device, stream, entry point tag).
 
-    The kernels leave their counters at zero, so a buffer is zeroed only when it is (re)allocated; each entry
-    point gets its own buffer because their layouts differ."""
+    The library needs no initialised workspace (every kernel writes what it later reads); each entry point gets
+    its own buffer because their layouts differ."""
     device = torch.device(device)
     if device.index is None:
         device = torch.device("cuda", torch.cuda.current_device())

@@ -82,7 +82,7 @@ class MoELayer:
             w = torch.empty((T, k), dtype=torch.float32, device=dev)
             head = (_lib.ptr(x2), T, _lib.ptr(self.norm_weight), self.eps, _lib.ptr(rt.weight),
                     _lib.ptr(rt.e_score_correction_bias), _lib.ptr(blk.slot_of), En, k, b)
-            tail = (_lib.ptr(h), _lib.ptr(r), _lib.ptr(inds), _lib.ptr(w))
+            tail = (_lib.ptr(h), _lib.ptr(r), _lib.ptr(inds), _lib.ptr(w), _lib.ptr(blk.status))
             if T <= pools.VERIFY_MAX:
                 nbytes = _lib.load().mimo_moe_layer_decode_workspace_size(T, En, k, b.hidden, b.inter)
                 ws = _lib.workspace(nbytes, dev, "layer_decode")
@@ -91,6 +91,8 @@ class MoELayer:
                 nbytes = _lib.load().mimo_moe_layer_prefill_workspace_size(T, En, k, b.n_slots, b.hidden, b.inter)
                 ws = _lib.workspace(nbytes, dev, "layer_prefill")
                 _lib.call("mimo_moe_layer_prefill", *head, *tail, _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+            if blk.partial:
+                blk.check_status("MoELayer")
         h = h.reshape(x.shape)
         out = (h,)
         if return_routes:

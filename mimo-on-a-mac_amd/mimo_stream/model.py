@@ -94,14 +94,33 @@ def prefill_dispatch(slot_inds, n_slots):
 
 
 class MoEBlock:
-    """One MoE layer: router, resident slot bank and expert -> slot table (slot_of None = identity)."""
+    """One MoE layer: router, resident slot bank and expert -> slot table (slot_of None = identity).
+
+    A table with experts outside the bank (entries outside [0, n_slots), e.g. a bank loaded for a subset of the
+    experts) makes the block partial: the kernels cannot read such an expert, so they flag it in the block's
+    device status word, and a partial block reads that word after every call (one synchronisation) and raises
+    ValueError when a route reached an expert with no slot, as the reference raises rather than compute with
+    the wrong expert (kernels.py:167-168; cache.py:45-46 loads the expert instead, which StreamedMoEBlock does).
+    A complete table needs no check: every expert has a slot and a row picks an expert at most once."""
 
     def __init__(self, router, bank, slot_of=None):
         self.router = router
         self.bank = bank
-        self.slot_of = None if slot_of is None else torch.as_tensor(slot_of, dtype=torch.int32).to(
-            router.weight.device).contiguous()
         self._bank_struct = bank_struct(bank)
+        dev = router.weight.device
+        self.slot_of = None if slot_of is None else torch.as_tensor(slot_of, dtype=torch.int32).to(dev).contiguous()
+        if self.slot_of is None:
+            self.partial = router.weight.shape[0] > self._bank_struct.n_slots
+        else:
+            if self.slot_of.shape != (router.weight.shape[0],):
+                raise ValueError(f"slot_of has {tuple(self.slot_of.shape)} entries for {router.weight.shape[0]} experts")
+            tab = self.slot_of.cpu()
+            self.partial = bool(((tab < 0) | (tab >= self._bank_struct.n_slots)).any())
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def check_status(self, what="MoEBlock"):
+        """Raise ValueError if the last call found a route to an expert with no slot (synchronises)."""
+        _lib.check_status(self.status, what)
 
     @property
     def n_slots(self):
@@ -111,9 +130,10 @@ class MoEBlock:
         inds = inds.to(torch.int64)
         return (self.slot_of[inds] if self.slot_of is not None else inds).to(torch.int32).contiguous()
 
-    def _moe_small(self, r2, inds, w):
+    def _moe_small(self, r2, inds, w, check=None):
         """T <= VERIFY_MAX rows with given routes (model.py:184-219): M == 1 rounds each expert's output to bf16
-        (_gather_m1), M >= 2 sums fp32 partials (distinct-expert kernels).  No host synchronisation."""
+        (_gather_m1), M >= 2 sums fp32 partials (distinct-expert kernels).  No host synchronisation unless the
+        grouping's status is checked (check, default: when the block is partial)."""
         _lib.require_cuda(r2)
         T, k = inds.shape
         if T > VERIFY_MAX:
@@ -129,22 +149,25 @@ class MoEBlock:
         ucnt = torch.empty(Umax, dtype=torch.int32, device=dev)
         uw = torch.empty((Umax, R), dtype=torch.float32, device=dev)
         gidx = torch.empty(T * k, dtype=torch.int32, device=dev)
-        nu = torch.empty(2, dtype=torch.int32, device=dev)
+        nu = torch.empty(1, dtype=torch.int32, device=dev)
         st = _lib.stream_ptr(dev)
         _lib.call("mimo_group_routes", _lib.ptr(slot_inds), _lib.ptr(w), None, T, k, R, S, _lib.ptr(uids),
-                  _lib.ptr(urows), _lib.ptr(ucnt), _lib.ptr(uw), _lib.ptr(gidx), _lib.ptr(nu[0:1]), _lib.ptr(nu[1:2]), st)
+                  _lib.ptr(urows), _lib.ptr(ucnt), _lib.ptr(uw), _lib.ptr(gidx), _lib.ptr(nu), _lib.ptr(self.status), st)
         x = r2.to(torch.bfloat16).contiguous()
         y = torch.empty((T, self._bank_struct.hidden), dtype=torch.bfloat16, device=dev)
         H, I = self._bank_struct.hidden, self._bank_struct.inter
         nbytes = _lib.load().mimo_moe_experts_workspace_size(T, Umax, R, H, I)
         ws = _lib.workspace(nbytes, dev, "experts")
         _lib.call("mimo_moe_experts", _lib.ptr(x), T, self._bank_struct, _lib.ptr(uids), _lib.ptr(urows), _lib.ptr(ucnt),
-                  _lib.ptr(uw), _lib.ptr(nu[0:1]), Umax, R, _lib.ptr(gidx), k, 1 if T == 1 else 0, _lib.ptr(y), None,
+                  _lib.ptr(uw), _lib.ptr(nu), Umax, R, _lib.ptr(gidx), k, 1 if T == 1 else 0, _lib.ptr(y), None,
                   None, _lib.ptr(ws), ws.numel(), st)
+        if self.partial if check is None else check:
+            self.check_status("MoEBlock._moe_small")
         return y
 
-    def _moe_prefill(self, r2, inds, w):
-        """Prefill with given routes (model.py:230-271): [T, H] bf16."""
+    def _moe_prefill(self, r2, inds, w, check=None):
+        """Prefill with given routes (model.py:230-271): [T, H] bf16.  The status is checked (one synchronisation)
+        when check, default: when the block is partial."""
         _lib.require_cuda(r2)
         T, k = inds.shape
         dev = r2.device
@@ -155,13 +178,16 @@ class MoEBlock:
         y = torch.empty((T, b.hidden), dtype=torch.bfloat16, device=dev)
         nbytes = _lib.load().mimo_moe_prefill_workspace_size(T, k, b.n_slots, b.hidden, b.inter)
         ws = _lib.workspace(nbytes, dev, "prefill")
-        _lib.call("mimo_moe_prefill", _lib.ptr(x), T, _lib.ptr(slot_inds), _lib.ptr(w), k, b, _lib.ptr(y), _lib.ptr(ws),
-                  ws.numel(), _lib.stream_ptr(dev))
+        _lib.call("mimo_moe_prefill", _lib.ptr(x), T, _lib.ptr(slot_inds), _lib.ptr(w), k, b, _lib.ptr(y),
+                  _lib.ptr(self.status), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev))
+        if self.partial if check is None else check:
+            self.check_status("MoEBlock._moe_prefill")
         return y
 
     def __call__(self, r, return_routes=False):
         """Router + experts for r bf16 [T, H] (model.py:303-336): T <= 8 runs the fused decode block, larger T
-        the prefill block.  Returns y bf16 [T, H] (and inds, w when return_routes)."""
+        the prefill block.  Returns y bf16 [T, H] (and inds, w when return_routes).  A partial block raises
+        ValueError when a row selected an expert that has no slot."""
         _lib.require_cuda(r)
         r2 = r.reshape(-1, r.shape[-1]).to(torch.bfloat16).contiguous()
         T = r2.shape[0]
@@ -178,7 +204,7 @@ class MoEBlock:
         w = torch.empty((T, k), dtype=torch.float32, device=dev)
         st = _lib.stream_ptr(dev)
         args = (_lib.ptr(r2), T, _lib.ptr(rt.weight), _lib.ptr(rt.e_score_correction_bias), _lib.ptr(self.slot_of), En, k,
-                b, _lib.ptr(y), _lib.ptr(inds), _lib.ptr(w))
+                b, _lib.ptr(y), _lib.ptr(inds), _lib.ptr(w), _lib.ptr(self.status))
         if T <= VERIFY_MAX:
             nbytes = _lib.load().mimo_moe_decode_workspace_size(T, En, k, b.hidden, b.inter)
             ws = _lib.workspace(nbytes, dev, "decode")
@@ -187,6 +213,8 @@ class MoEBlock:
             nbytes = _lib.load().mimo_moe_prefill_block_workspace_size(T, En, k, b.n_slots, b.hidden, b.inter)
             ws = _lib.workspace(nbytes, dev, "prefill_block")
             _lib.call("mimo_moe_prefill_block", *args, _lib.ptr(ws), ws.numel(), st)
+        if self.partial:
+            self.check_status("MoEBlock")
         return (y, inds, w) if return_routes else y
 
     def forward_residual(self, x, r):

@@ -121,7 +121,7 @@ class StreamedMoEBlock:
             self._fill(self.block.bank, loads)
             if loads:
                 self._push_table()
-            y = self.block._moe_small(r2, inds, w)
+            y = self.block._moe_small(r2, inds, w, check=False)   # resolve gave every selected expert a slot
             self.decode_calls += 1
             if self.decode_calls % self.decay_every == 0:
                 self.cache.decay()
@@ -133,7 +133,7 @@ class StreamedMoEBlock:
         needed = np.unique(inds_h)
         held = self.cache.slot_of[needed]
         if (held >= 0).all():
-            return self.block._moe_prefill(r2, inds, w)
+            return self.block._moe_prefill(r2, inds, w, check=False)
         b = self.block._bank_struct
         if self._stage is None:
             self._stage = pools.alloc_bank(self.cache.E, b.hidden, b.inter, device=self.dev)
@@ -148,4 +148,4 @@ class StreamedMoEBlock:
             for k, v in self.block.bank.items():
                 torch.index_select(v, 0, src, out=stage[k][: res.size])
         self._fill(stage, [(int(e), int(stage_of[e])) for e in mis])
-        return MoEBlock(self.block.router, stage, slot_of=stage_of)._moe_prefill(r2, inds, w)
+        return MoEBlock(self.block.router, stage, slot_of=stage_of)._moe_prefill(r2, inds, w, check=False)

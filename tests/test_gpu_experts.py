@@ -172,8 +172,8 @@ def test_slot_table_indirection(rng, tiny_pool):
 
 
 def test_workspace_reuse_across_shapes(rng, tiny_pool, mimo_pool):
-    """One cached workspace serves calls of different shapes: the completion counters sit at fixed offsets,
-    so a call after a differently-shaped call still finds them at zero (regression test)."""
+    """One cached workspace serves calls of different shapes: a call after differently-shaped calls that left
+    their own data in it gives the same bits (no kernel reads workspace it did not write in the same call)."""
     tbank, tpool = tiny_pool
     mbank, _ = mimo_pool
     tblk, _, _ = _block(rng, tbank, 256, 8, 2)

@@ -101,7 +101,7 @@ def test_layer_fused_equals_composition(rng, T, shape):
     blk, b = layer.block, layer.block._bank_struct
     xi = x.clone()
     args = (_lib.ptr(xi), T, _lib.ptr(layer.norm_weight), EPS, _lib.ptr(blk.router.weight),
-            _lib.ptr(blk.router.e_score_correction_bias), None, E, k, b, _lib.ptr(xi), None, None, None)
+            _lib.ptr(blk.router.e_score_correction_bias), None, E, k, b, _lib.ptr(xi), None, None, None, None)
     if T <= 8:
         nb = _lib.load().mimo_moe_layer_decode_workspace_size(T, E, k, H, I)
         ws = torch.zeros(nb, dtype=torch.uint8, device="cuda")
