@@ -43,21 +43,28 @@ def swiglu_bf16(g_f32, u_f32):
 
 
 class ExpertPool:
-    """Slot pool {gate_w, gate_s, up_w, up_s, down_w, down_s} (model.py:32-45) with cached exact dequant."""
+    """Slot pool {gate_w, gate_s, up_w, up_s, down_w, down_s} (model.py:32-45) with exact dequantisation.
 
-    def __init__(self, pools):
+    cache=True keeps every dequantised projection (float64, 8 bytes per weight): for pools that are used many
+    times; cache=False dequantises on each use (for sub-pools of many MiMo-sized experts, each used once)."""
+
+    def __init__(self, pools, cache=True):
         self.p = {k: np.asarray(v) for k, v in pools.items()}
-        self._cache = {}
+        self._cache = {} if cache else None
 
     def weights(self, name, slot):
+        """float64 [out, in]: the exactly dequantised weights of one slot."""
         key = (name, int(slot))
-        if key not in self._cache:
-            self._cache[key] = mxfp4.dequantize_mxfp4(self.p[f"{name}_w"][slot], self.p[f"{name}_s"][slot])
-        return self._cache[key]
+        if self._cache is not None and key in self._cache:
+            return self._cache[key]
+        W = mxfp4.dequantize_mxfp4_f64(self.p[f"{name}_w"][slot], self.p[f"{name}_s"][slot])
+        if self._cache is not None:
+            self._cache[key] = W
+        return W
 
     def dot(self, name, slot, rows):
         """rows float [n, in] -> fp32 [n, out]: float64 accumulation, one rounding to fp32."""
-        W = self.weights(name, slot).astype(np.float64)
+        W = self.weights(name, slot)
         return (np.asarray(rows, dtype=np.float64) @ W.T).astype(np.float32)
 
 
@@ -167,10 +174,10 @@ def reference_fp32(x, pool, slot_inds, scores):
     out = np.zeros((M, H))
     for m in range(M):
         for e, s in zip(slot_inds[m], scores[m]):
-            g = pool.weights("gate", e).astype(np.float64) @ x[m]
-            u = pool.weights("up", e).astype(np.float64) @ x[m]
+            g = pool.weights("gate", e) @ x[m]
+            u = pool.weights("up", e) @ x[m]
             hh = (g / (1.0 + np.exp(-g))) * u
-            out[m] += float(s) * (pool.weights("down", e).astype(np.float64) @ hh)
+            out[m] += float(s) * (pool.weights("down", e) @ hh)
     return out
 
 

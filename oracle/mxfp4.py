@@ -110,6 +110,26 @@ def dequantize_mxfp4(q, s):
     return out.reshape(vals.shape).astype(np.float32)
 
 
+# the two E2M1 values of every byte of packed nibbles: [byte, 0] = low nibble (the earlier element), [byte, 1] = high
+_BYTE_PAIRS = np.stack([E2M1_VALUES[np.arange(256) & 15], E2M1_VALUES[np.arange(256) >> 4]], 1).astype(np.float64)
+
+
+def dequantize_mxfp4_f64(q, s):
+    """dequantize_mxfp4 in float64, for the oracle's dot products: the same values (an E2M1 value times a power
+    of two is exact in both types) wherever they fit float32, i.e. for every scale byte but 253 and 254, whose
+    largest products the float32 form overflows to +-inf; computed through a byte -> value-pair table instead of
+    one nibble at a time.  Elements of a uint32 word are its nibbles from the low end, i.e. its little-endian
+    bytes' low then high nibbles (kernels.py:5)."""
+    q = np.asarray(q, dtype=np.uint32)
+    K = q.shape[-1] * 8
+    b = np.ascontiguousarray(q.astype("<u4", copy=False)).view(np.uint8)
+    out = np.take(_BYTE_PAIRS, b, axis=0).reshape(*q.shape[:-1], K // 32, 32)
+    sc = e8m0_to_float(s).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        out *= sc[..., None]
+    return out.reshape(*q.shape[:-1], K)
+
+
 # ---------------------------------------------------------------- E4M3 + hi/lo activation split
 def e4m3_to_float(c):
     """OCP E4M3 (bias 7, no inf, S.1111.111 = NaN) code -> float32."""

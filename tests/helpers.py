@@ -21,13 +21,13 @@ def to_dev_bf16(a, device="cuda"):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).to(device)
 
 
-def pool_np(bank):
+def pool_np(bank, cache=True):
     """Device bank dict -> oracle ExpertPool (uint32 / uint8 numpy)."""
     p = {}
     for k, v in bank.items():
         a = v.cpu().numpy()
         p[k] = a.view(np.uint32) if k.endswith("_w") else a
-    return ox.ExpertPool(p)
+    return ox.ExpertPool(p, cache=cache)
 
 
 def rand_bf16(rng, shape, scale=1.0):

@@ -1,0 +1,227 @@
+"""Parity at the MiMo-V2.6-Flash shapes of every benchmarked workload, against the oracle, with the errors recorded.
+
+Workloads (hidden 4096, 256 experts, intermediate 2048, top-8, MXFP4 group 32; the tiny layer is 8 experts, top-2,
+hidden 256, intermediate 512):
+  tiny      the plumbing layer, decode (4 rows) and prefill (32 tokens), every element compared.
+  1 row     one MoE layer, all 256 experts resident, decode of single rows (the M = 1 path, model.py:173-182):
+            routes bit-exact given the logits, y against the oracle on a sub-pool of the selected experts.
+  rows      the same layer at 2, 4 and 8 rows with routing steered so consecutive rows share experts (the
+            distinct-expert kernels, kernels.py:176-199).
+  prefill   Zipf(1.1) routes at 512, 2048 and 4096 tokens (4096 = the reference server's chunk,
+            engine/server.py:34: 32,768 slot-sorted routes, the size bench/scripts/gather_qmm_sorted_check.py:36
+            checks).  Every token is compared: the combine weights are nonzero only on routes to a set Q of up to
+            16 experts spread over the popularity ranks (the most popular one, cut into many 96-route tiles, down
+            to experts with a single route), so the oracle needs only Q's weights while every tile of those
+            experts, both tile shapes and multi-term combines are checked; tokens with no route into Q must come
+            out exactly zero.  A second call with every weight nonzero is compared on 4 random tokens.
+  stack     48 layers (164 GB of experts resident), one decode step through every layer at 1 and 4 rows: layers
+            0, 23 and 47 against the oracle, every layer bit-identical on a rerun.
+
+Bars (the block tests' own): max|dy| / max|y| < 1e-2 and >= 99% of elements within two bf16 ulps of the oracle;
+< 2e-2 against the reference test's unrounded fp32 oracle (engine/tests/test_kernels.py:79).  Max-abs and max-rel
+errors per workload go to the JSON file named by MIMO_PARITY_REPORT when it is set."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, bf16_np, pool_np, rand_bf16, to_dev_bf16, zipf_routes
+from oracle import experts as ox, mxfp4 as oq, routing as orr
+
+pytestmark = pytest.mark.gpu
+H, I, E, K = 4096, 2048, 256, 8
+LAYERS = 48
+REPORT = []
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _report():
+    yield
+    path = os.environ.get("MIMO_PARITY_REPORT")
+    if path and REPORT:
+        with open(path, "w") as f:
+            json.dump(REPORT, f, indent=1)
+
+
+def _record(workload, got, ref, fp32_ref=None, **info):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rel, frac = assert_bf16_close(got, ref, what=workload)
+    d = np.abs(got - ref)
+    row = {"workload": workload, "elements": int(got.size), "max_abs": float(d.max()),
+           "max_abs_ref": float(np.abs(ref).max()), "max_rel": rel, "within_2ulp": frac,
+           "exact": float(np.mean(d == 0))}
+    if fp32_ref is not None:
+        e32 = ox.rel_err(got, fp32_ref)
+        assert e32 < 2e-2, (workload, e32)
+        row["rel_vs_fp32"] = e32
+    row.update(info)
+    REPORT.append(row)
+    print(json.dumps(row))
+    return row
+
+
+def _subpool(bank, slots):
+    """Oracle pool of the given slots only (their bytes copied from the device), and slot -> sub-slot."""
+    need = np.unique(np.asarray(slots).reshape(-1))
+    idx = torch.from_numpy(need.astype(np.int64)).cuda()
+    pool = pool_np({k: v.index_select(0, idx) for k, v in bank.items()})
+    remap = np.full(int(need.max()) + 1, -1, np.int64)
+    remap[need] = np.arange(need.size)
+    return pool, remap
+
+
+@pytest.fixture(scope="module")
+def stack():
+    from mimo_stream import MoEBlock, Router, kernels, pools
+    torch.cuda.empty_cache()
+    free, _ = torch.cuda.mem_get_info()
+    need = LAYERS * E * pools.EXPERT_BYTES + (8 << 30)
+    if free < need:
+        pytest.skip(f"the 48-layer stack needs {need / 1e9:.0f} GB of free HBM, {free / 1e9:.0f} GB free")
+    blocks = []
+    for l in range(LAYERS):
+        bank = pools.random_bank(E, seed=900 + l)
+        r = Router(H, E, K)
+        r.weight.copy_(kernels.random_bf16((E, H), seed=7000 + l, stddev=0.02))
+        r.e_score_correction_bias.copy_(kernels.random_bf16((E,), seed=8000 + l, stddev=1e-3).float())
+        blocks.append(MoEBlock(r, bank))
+    torch.cuda.synchronize()
+    yield blocks
+    del blocks
+    torch.cuda.empty_cache()
+
+
+def _steered(rng, blk, M):
+    import bench
+    W = blk.router.weight.float().cpu().numpy()
+    return oq.round_bf16(bench.steered_rows(rng, W, bench.controlled_sets(rng, M)))
+
+
+def _check_decode(blk, x, what, **info):
+    """Fused decode of rows x on blk: routes bit-exact given the logits, y against the oracle on a sub-pool."""
+    M = x.shape[0]
+    xd = to_dev_bf16(x)
+    y, inds, w = blk(xd, return_routes=True)
+    logits, i2, w2 = blk.router.logits_and_routes(xd)
+    assert torch.equal(i2, inds) and torch.equal(w2, w), "the router entry point and the block route alike"
+    lg = logits.cpu().numpy()
+    bias = blk.router.e_score_correction_bias.cpu().numpy()
+    oi, ow = orr.select_topk(lg, bias, K)
+    gi, gw = inds.cpu().numpy(), w.cpu().numpy()
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gw, ow)
+    ref_logits = orr.router_logits(x, blk.router.weight.float().cpu().numpy())
+    assert np.abs(lg - ref_logits).max() <= 1e-5 * np.abs(ref_logits).max() + 1e-6
+    pool, remap = _subpool(blk.bank, gi)
+    si = remap[gi]
+    if M == 1:
+        oy = ox.gather_m1(x[0], pool, si[0], gw[0])[None]
+    else:
+        uids, urows, ucnt, uw, gidx = orr.group_routes(si, gw, R=8)
+        oy, _, _ = ox.moe_experts(x, pool, uids, urows, ucnt, uw, gidx, K, R=8)
+    f32 = ox.reference_fp32(x, pool, si, gw)
+    return _record(what, bf16_np(y), oy, f32, rows=M, distinct_experts=int(np.unique(gi).size), **info), y
+
+
+def test_tiny_layer_every_element(rng):
+    """The plumbing layer (8 experts, top-2, hidden 256, intermediate 512, 4 rows): decode and prefill blocks."""
+    from mimo_stream import MoEBlock, Router, pools
+    bank = pools.random_bank(8, seed=0, hidden=256, inter=512)
+    r = Router(256, 8, 2)
+    W = rand_bf16(rng, (8, 256), 0.02)
+    r.weight.copy_(to_dev_bf16(W))
+    blk = MoEBlock(r, bank)
+    pool = pool_np(bank)
+    x = rand_bf16(rng, (4, 256))
+    y, inds, w = blk(to_dev_bf16(x), return_routes=True)
+    gi, gw = inds.cpu().numpy(), w.cpu().numpy()
+    uids, urows, ucnt, uw, gidx = orr.group_routes(gi, gw, R=8)
+    oy, _, _ = ox.moe_experts(x, pool, uids, urows, ucnt, uw, gidx, 2, R=8)
+    _record("tiny decode 4 rows", bf16_np(y), oy, ox.reference_fp32(x, pool, gi, gw))
+    xp = rand_bf16(rng, (32, 256))
+    yp, ip, wp = blk(to_dev_bf16(xp), return_routes=True)
+    ipn, wpn = ip.cpu().numpy(), wp.cpu().numpy()
+    _record("tiny prefill 32 tokens", bf16_np(yp), ox.moe_prefill(xp, pool, ipn, wpn),
+            ox.reference_fp32(xp, pool, ipn, wpn))
+
+
+def test_decode_one_row_256_experts(rng, stack):
+    """One row at a time through the 256-expert layer (the fast single-row selection: expert ids are slots)."""
+    blk = stack[0]
+    for step in range(3):
+        x = rand_bf16(rng, (1, H))
+        _check_decode(blk, x, f"decode 1 row, 256 experts, step {step}")
+
+
+@pytest.mark.parametrize("M", [2, 4, 8])
+def test_decode_rows_256_experts(rng, stack, M):
+    _check_decode(stack[1], _steered(rng, stack[1], M), f"decode {M} rows, 256 experts")
+
+
+def _q_experts(counts):
+    """Up to 16 experts over the popularity ranks of this batch: the most popular first, down to single-route ones."""
+    order = np.argsort(-counts, kind="stable")
+    order = order[counts[order] > 0]
+    ranks = [0, 1, 2, 3, 5, 8, 12, 20, 32, 50, 80, 120, 170, 220]
+    q = [int(order[r]) for r in ranks if r < order.size]
+    singles = order[counts[order] == 1]
+    if singles.size:
+        q.append(int(singles[0]))
+    q.append(int(order[-1]))
+    return np.unique(np.array(q, np.int64))
+
+
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_prefill_zipf_every_token(rng, stack, T):
+    blk = stack[2]
+    x = rand_bf16(rng, (T, H))
+    inds = zipf_routes(rng, T, E, K)
+    counts = np.bincount(inds.reshape(-1), minlength=E)
+    Q = _q_experts(counts)
+    inQ = np.isin(inds, Q)
+    w = rng.random((T, K)).astype(np.float32)
+    wq = np.where(inQ, w, 0.0).astype(np.float32)
+    xd, idd = to_dev_bf16(x), torch.from_numpy(inds).cuda()
+    y = blk._moe_prefill(xd, idd, torch.from_numpy(wq).cuda())
+    y2 = blk._moe_prefill(xd, idd, torch.from_numpy(wq).cuda())
+    assert torch.equal(y, y2), "run-to-run bit-identical"
+    yn = bf16_np(y)
+    touched = inQ.any(1)
+    assert np.all(yn[~touched] == 0.0), "tokens with no weighted route come out exactly zero"
+    pool, remap = _subpool(blk.bank, Q)
+    tok, j = np.nonzero(inQ)
+    Yq = ox.pair_outputs(x, pool, tok, remap[inds[tok, j]])
+    Y = np.zeros((T, K, H), np.float32)
+    Y[tok, j] = Yq
+    oy = ox.weighted_sum_bf16(Y, wq)
+    top = int(Q[np.argmax(counts[Q])])
+    _record(f"prefill {T} tokens, routes to {Q.size} experts", yn, oy, tokens=T, q_experts=int(Q.size),
+            q_routes=int(inQ.sum()), tokens_compared=int(T), top_expert_routes=int(counts[top]),
+            top_expert_wide_tiles=int(-(-counts[top] // 96)), experts_touched=int((counts > 0).sum()))
+    # every weight nonzero: the full k-term combine of 4 random tokens
+    wf = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    yf = bf16_np(blk._moe_prefill(xd, idd, torch.from_numpy(wf).cuda()))
+    sample = rng.choice(T, 4, replace=False)
+    pool, remap = _subpool(blk.bank, inds[sample])
+    oyf = np.stack([ox.gather_m1(x[t], pool, remap[inds[t]], wf[t]) for t in sample])
+    _record(f"prefill {T} tokens, all weights, 4 tokens", yf[sample], oyf,
+            ox.reference_fp32(x[sample], pool, remap[inds[sample]], wf[sample]), tokens=T)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_stack48_decode_step(rng, stack, M):
+    """One decode step through all 48 resident layers (per-layer steered hidden states): every layer's y is
+    bit-identical on a rerun, layers 0, 23 and 47 match the oracle."""
+    xs = [_steered(rng, blk, M) for blk in stack]
+    xd = [to_dev_bf16(x) for x in xs]
+    ys = [blk(x) for blk, x in zip(stack, xd)]
+    again = [blk(x) for blk, x in zip(stack, xd)]
+    torch.cuda.synchronize()
+    for l, (a, b) in enumerate(zip(ys, again)):
+        assert torch.equal(a, b), f"layer {l} differs on a rerun"
+    for l in (0, 23, 47):
+        row, y = _check_decode(stack[l], xs[l], f"48-layer stack decode {M} rows, layer {l}", layer=l)
+        assert torch.equal(y, ys[l]), f"layer {l}: the checked call and the stack step differ"

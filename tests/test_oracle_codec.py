@@ -89,6 +89,28 @@ def test_quantize_idempotent_on_grid():
     np.testing.assert_array_equal(mxfp4.dequantize_mxfp4(q2, s2), deq)
 
 
+def test_dequantize_f64_table_equals_nibble_definition():
+    """The byte-table float64 dequantisation (used by the oracle's dot products) gives exactly the values of the
+    nibble-by-nibble definition: every byte value in both nibble positions, every scale byte (0 and 255
+    included, NaN where the scale is NaN).  Scales 253 and 254 put +-3 .. +-6 above the float32 range: there the
+    float32 definition overflows to +-inf and the float64 form keeps the exact product."""
+    rng = np.random.default_rng(5)
+    q = rng.integers(0, 2 ** 32, (256, 64), dtype=np.uint64).astype(np.uint32)
+    q[0] = np.arange(256, dtype=np.uint32).reshape(64, 4) @ np.array([1, 256, 65536, 1 << 24], np.uint32)
+    s = np.tile(np.arange(256, dtype=np.uint8)[:, None], (1, 16))
+    a = mxfp4.dequantize_mxfp4(q, s).astype(np.float64)
+    b = mxfp4.dequantize_mxfp4_f64(q, s)
+    assert b.dtype == np.float64 and b.shape == a.shape
+    np.testing.assert_array_equal(np.isnan(a), np.isnan(b))
+    ok = ~np.isnan(a) & ~np.isinf(a)
+    np.testing.assert_array_equal(a[ok], b[ok])
+    np.testing.assert_array_equal(np.signbit(a[ok]), np.signbit(b[ok]))   # -0 codes stay -0
+    big = np.isinf(a)
+    assert big.any() and np.all(s.repeat(32, 1)[big] >= 253)
+    vals = mxfp4.E2M1_VALUES[mxfp4.unpack_nibbles(q)].astype(np.float64)
+    np.testing.assert_array_equal(b[big], np.ldexp(vals[big], s.repeat(32, 1)[big].astype(np.int64) - 127))
+
+
 def test_e4m3_decode_matches_torch():
     codes = np.arange(256, dtype=np.uint8)
     theirs = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
