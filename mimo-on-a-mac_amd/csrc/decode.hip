@@ -618,18 +618,20 @@ struct ExpertsWs {
   uint8_t *hq_hi, *hq_lo, *hq_hs, *hq_ls;
   float* part;
 };
-static ExpertsWs carve_experts(Carve& c, int M, int Umax, int R, int H, int I) {
-  ExpertsWs w;
+// intermediates: room for the bf16 h and the fp32 partials, written only when a caller of mimo_moe_experts asks
+// for them (the fused decode never does)
+static ExpertsWs carve_experts(Carve& c, int M, int Umax, int R, int H, int I, bool intermediates) {
+  ExpertsWs w{};
   w.xq_hi = c.take<uint8_t>((size_t)M * H);
   w.xq_lo = c.take<uint8_t>((size_t)M * H);
   w.xq_hs = c.take<uint8_t>((size_t)M * H / 32);
   w.xq_ls = c.take<uint8_t>((size_t)M * H / 32);
-  w.h = c.take<uint16_t>((size_t)Umax * R * I);
+  if (intermediates) w.h = c.take<uint16_t>((size_t)Umax * R * I);
   w.hq_hi = c.take<uint8_t>((size_t)Umax * R * I);
   w.hq_lo = c.take<uint8_t>((size_t)Umax * R * I);
   w.hq_hs = c.take<uint8_t>((size_t)Umax * R * I / 32);
   w.hq_ls = c.take<uint8_t>((size_t)Umax * R * I / 32);
-  w.part = c.take<float>((size_t)Umax * R * H);
+  if (intermediates) w.part = c.take<float>((size_t)Umax * R * H);
   return w;
 }
 
@@ -741,7 +743,7 @@ extern "C" {
 
 size_t mimo_moe_experts_workspace_size(int M, int Umax, int R, int H, int I) {
   Carve c(nullptr, 0);
-  carve_experts(c, M, Umax, R, H, I);
+  carve_experts(c, M, Umax, R, H, I, true);
   return c.off;
 }
 
@@ -761,7 +763,7 @@ int mimo_moe_experts(const uint16_t* x, int M, const mimo_bank* bank, const int3
                "moe_experts: x, y, part_out must be 16-byte aligned");
   const int H = bank->hidden, I = bank->inter;
   Carve c(ws, ws_bytes);
-  ExpertsWs w = carve_experts(c, M, Umax, R, H, I);
+  ExpertsWs w = carve_experts(c, M, Umax, R, H, I, true);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_experts: workspace too small (need %zu)", c.off);
   hipStream_t st = as_stream(stream);
   rc = launch_quantize_fp8_hilo(x, M, H, w.xq_hi, w.xq_hs, w.xq_lo, w.xq_ls, st);
@@ -808,7 +810,7 @@ size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
   int32_t *inds, *uids, *urows, *ucnt, *nu, *st;
   uint32_t* gidx;
   carve_decode(c, M, E, k, Umax, kDecodeR, &l, &s, &kk, &inds, &w, &uids, &urows, &ucnt, &uw, &gidx, &nu, &st);
-  carve_experts(c, M, Umax, kDecodeR, H, I);
+  carve_experts(c, M, Umax, kDecodeR, H, I, false);
   return c.off;
 }
 
@@ -836,7 +838,7 @@ static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float
   uint32_t* gidx;
   carve_decode(c, M, E, k, Umax, kDecodeR, &logits, &scores, &keys, &inds, &w, &uids, &urows, &ucnt, &uw,
                &gidx, &nu, &status);
-  ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I);
+  ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I, false);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_decode: workspace too small (need %zu)", c.off);
 
   RouterSmallArgs ra{};
@@ -898,3 +900,4 @@ int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, floa
 }
 
 }  // extern "C"
+
