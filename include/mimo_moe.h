@@ -199,6 +199,19 @@ int mimo_moe_layer_prefill(const uint16_t* x, int T, const uint16_t* norm_w, flo
                            void* ws, size_t ws_bytes, void* stream);
 size_t mimo_moe_layer_prefill_workspace_size(int T, int E, int k, int n_slots, int H, int I);
 
+/* No counterpart in the reference: mimo_moe_layer_decode for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The same kernels, with the
+ * workspace in a scratch array the library holds on each GPU (MIMO_NOALLOC_SCRATCH_BYTES, kept until the process
+ * ends); the call itself allocates nothing (per-kernel event timing is skipped for it).  Batches whose workspace
+ * (mimo_moe_layer_decode_workspace_size) exceeds the scratch are refused with MIMO_ERR_WORKSPACE; MiMo's largest,
+ * 8 rows of 256 experts, needs about 2.3 MB.  Every call on one GPU uses that GPU's one scratch array: calls that
+ * overlap on one GPU (two host threads, or two streams without an ordering between them) race. */
+#define MIMO_NOALLOC_SCRATCH_BYTES (4u << 20)
+int mimo_moe_layer_decode_noalloc(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
+                                  const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank,
+                                  uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out,
+                                  int32_t* status_out, void* stream);
+
 /* ---------------------------------------------------------------- measurement */
 
 /* No counterpart in the reference: per-kernel timing for benchmarks.  While enabled, every kernel launch is

@@ -41,6 +41,9 @@ static bool g_prof_open_owns = true;
 static int g_prof_chain = 0;
 static hipEvent_t g_prof_last_end = nullptr;
 static hipStream_t g_prof_last_stream = nullptr;
+static thread_local int t_prof_suspend = 0;
+
+void prof_suspend(bool on) { t_prof_suspend += on ? 1 : -1; }
 
 static hipEvent_t prof_event() {
   if (!g_prof_pool.empty()) {
@@ -54,7 +57,7 @@ static hipEvent_t prof_event() {
 }
 
 void prof_begin(hipStream_t st, const char* name) {
-  if (!g_prof_on) return;
+  if (!g_prof_on || t_prof_suspend) return;
   std::lock_guard<std::mutex> lk(g_prof_mu);
   if (g_prof_chain && g_prof_last_end && g_prof_last_stream == st) {
     g_prof_open = name;
@@ -74,7 +77,7 @@ void prof_begin(hipStream_t st, const char* name) {
 }
 
 void prof_end(hipStream_t st) {
-  if (!g_prof_on) return;
+  if (!g_prof_on || t_prof_suspend) return;
   std::lock_guard<std::mutex> lk(g_prof_mu);
   if (!g_prof_open) return;
   hipEvent_t e = prof_event();
@@ -92,7 +95,7 @@ void prof_end(hipStream_t st) {
 }
 
 void prof_chain(bool on) {
-  if (!g_prof_on) return;
+  if (!g_prof_on || t_prof_suspend) return;
   std::lock_guard<std::mutex> lk(g_prof_mu);
   g_prof_chain += on ? 1 : -1;
   if (on && g_prof_chain == 1) g_prof_last_end = nullptr;     // the chain starts with a fresh begin event

@@ -15,6 +15,8 @@
 //   FP8 operand: bytes 0-15 hold K = 16g .. 16g+15, bytes 16-31 hold K = 64+16g .. 64+16g+15.
 //   scale of K-block b (32 wide) of row/column i comes from lane i + 16b (byte 0).
 //   D: lane l holds column l % 16, rows 4g .. 4g+3.
+#include <mutex>
+
 #include "device.h"
 #include "host.h"
 #include "layer.h"
@@ -901,3 +903,55 @@ int mimo_moe_layer_decode(const uint16_t* x, int M, const uint16_t* norm_w, floa
 
 }  // extern "C"
 
+// ------------------------------------------------------------------ layer decode without a caller workspace
+// The workspace of mimo_moe_layer_decode_noalloc: a file-scope device array, one copy per GPU, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel (in host code it names a host-side
+// stand-in); it uses the device address that hipGetSymbolAddress returns for the current device.
+namespace mimo {
+constexpr size_t kNoAllocScratchBytes = MIMO_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// Device address of this GPU's scratch array, looked up once per device (with that device current).
+static int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(MIMO_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  MIMO_REQUIRE(dev >= 0 && dev < 64, MIMO_ERR_HIP, "device %d: at most 64 devices", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(MIMO_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MIMO_OK;
+}
+}  // namespace mimo
+
+extern "C" {
+
+int mimo_moe_layer_decode_noalloc(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const uint16_t* Wg,
+                                  const float* bias, const int32_t* slot_of, int E, int k, const mimo_bank* bank,
+                                  uint16_t* h, uint16_t* r_out, int32_t* inds_out, float* w_out, int32_t* status_out,
+                                  void* stream) {
+  ProfSuspend no_events;   // event timing would create events: this entry point allocates nothing
+  MIMO_REQUIRE(bank, MIMO_ERR_ARG, "moe_layer_decode_noalloc: null bank");
+  MIMO_REQUIRE(M >= 1 && M <= 8 && k >= 1 && k <= 8 && E >= 1 && E <= 1024, MIMO_ERR_SHAPE,
+               "moe_layer_decode_noalloc: need 1 <= M <= 8, 1 <= k <= 8, E <= 1024");
+  const size_t need = mimo_moe_layer_decode_workspace_size(M, E, k, bank->hidden, bank->inter);
+  MIMO_REQUIRE(need <= kNoAllocScratchBytes, MIMO_ERR_WORKSPACE,
+               "moe_layer_decode_noalloc: M=%d, E=%d, k=%d, hidden %d, intermediate %d need %zu bytes of scratch; "
+               "the built-in scratch holds %zu (use mimo_moe_layer_decode with a workspace)", M, E, k, bank->hidden,
+               bank->inter, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return mimo_moe_layer_decode(x, M, norm_w, eps, Wg, bias, slot_of, E, k, bank, h, r_out, inds_out, w_out,
+                               status_out, ws, kNoAllocScratchBytes, stream);
+}
+
+}  // extern "C"

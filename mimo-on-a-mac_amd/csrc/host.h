@@ -28,6 +28,12 @@ inline int check_launch(const char* what) {
 void prof_begin(hipStream_t st, const char* name);
 void prof_end(hipStream_t st);
 void prof_chain(bool on);
+// While a ProfSuspend lives on this thread, launches are not timed (no events are created or recorded).
+void prof_suspend(bool on);
+struct ProfSuspend {
+  ProfSuspend() { prof_suspend(true); }
+  ~ProfSuspend() { prof_suspend(false); }
+};
 // Multi-kernel entry points time their kernels back to back: each begin is the previous kernel's end event.
 struct ProfChain {
   ProfChain() { prof_chain(true); }

@@ -61,6 +61,7 @@ SIGNATURES = {
     "mimo_moe_layer_decode_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "mimo_moe_layer_prefill": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, P, SZ, P]),
     "mimo_moe_layer_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "mimo_moe_layer_decode_noalloc": (I32, [P, I32, P, F32, P, P, P, I32, I32, BANKP, P, P, P, P, P, P]),
     "mimo_profile_enable": (I32, [I32]),
     "mimo_profile_read": (I32, [I32, P, P, P]),
 }
