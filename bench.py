@@ -64,6 +64,10 @@ def parse():
                          "SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE, using the kernel durations of a "
                          "--kernel-trace run of the same payload (second argument)")
     ap.add_argument("--mfma-trace", metavar="TRACE_DIR", help="kernel-trace directory for --mfma-parse")
+    ap.add_argument("--trace-parse", metavar="TRACE_DIR",
+                    help="summarise a rocprofv3 --kernel-trace run of this benchmark: a markdown table per kernel "
+                         "and grid on stdout, and the headline kernel's average duration (and its interval from "
+                         "the previous kernel's end, what the live HIP events measure) to profiles/trace.json")
     return ap.parse_args()
 
 
@@ -259,6 +263,61 @@ def stack_case(layers, M, tokens, device, seed):
             "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+HEADLINE_KERNEL = ("decode_gateup_kernel<8, true, false>", 32768, 8)     # 1-row decode: 64 x 8 blocks of 512
+
+
+def trace_parse(d):
+    """rocprofv3 kernel trace of bench.py -> markdown on stdout, headline figures to profiles/trace.json."""
+    import collections
+    import csv
+    rows = []
+    for name in os.listdir(d):
+        if name.endswith("kernel_trace.csv"):
+            with open(os.path.join(d, name)) as f:
+                rows += list(csv.DictReader(f))
+    if not rows:
+        raise SystemExit(f"{d}: no kernel_trace.csv")
+    rows.sort(key=lambda r: (r["Queue_Id"], int(r["Start_Timestamp"])))
+    acc = collections.defaultdict(list)
+    gap = []
+    prev_end = {}
+    for r in rows:
+        q, t0, t1 = r["Queue_Id"], int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        n = r["Kernel_Name"]
+        if "mimo::" in n:
+            key = (n.split("(")[0].replace("void ", "").replace("mimo::", ""), int(r["Grid_Size_X"]),
+                   int(r["Grid_Size_Y"]), int(r["Workgroup_Size_X"]))
+            acc[key].append((t1 - t0) / 1e3)
+            if key[:3] == HEADLINE_KERNEL and q in prev_end:
+                gap.append((t1 - prev_end[q]) / 1e3)
+        prev_end[q] = t1
+    print("| kernel | grid (threads) | block | dispatches | avg µs | min µs | max µs |\n|---|---|---|---|---|---|---|")
+    for (n, gx, gy, wx), v in sorted(acc.items()):
+        print(f"| `{n}` | {gx}×{gy} | {wx} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} |")
+    head = [v for k, v in acc.items() if k[:3] == HEADLINE_KERNEL]
+    if head:
+        v = head[0]
+        out = {"decode_gateup_kernel:decode_m1": {
+            "avg_us": sum(v) / len(v), "launches": len(v),
+            "after_previous_end_us": sum(gap) / len(gap) if gap else None}}
+        print(f"\nHeadline kernel `{HEADLINE_KERNEL[0]}` (grid {HEADLINE_KERNEL[1]}×{HEADLINE_KERNEL[2]}): "
+              f"{len(v)} dispatches, average duration {out['decode_gateup_kernel:decode_m1']['avg_us']:.2f} µs; "
+              f"average interval from the previous kernel's end on its queue to its own end "
+              f"{out['decode_gateup_kernel:decode_m1']['after_previous_end_us']:.2f} µs (the interval the "
+              f"benchmark's chained HIP events measure).")
+        with open(os.path.join(ROOT, "profiles", "trace.json"), "w") as f:
+            json.dump(out, f, indent=1)
+
+
+def trace_from_profiles(key):
+    path = os.path.join(ROOT, "profiles", "trace.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+
+
 def traffic_from_profiles(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 counters (committed summary), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -270,40 +329,35 @@ def traffic_from_profiles(kernel, workload):
         return None
 
 
-def cpu_baseline(layers, seconds):
-    """The numpy oracle (CPU restatement of Router + _gather_m1, model.py:58-65, :173-182) on M = 1 decode
-    steps of the same layers, one thread, for about `seconds`; returns GB/s with the same byte accounting."""
+def cpu_baseline(layers, seconds, n_layers=2):
+    """The one-row MoE-layer decode (Router + _gather_m1, model.py:58-65, :173-182) on the host CPU: the fp32
+    PyTorch restatement oracle.cpu_decode on every thread PyTorch is given (OMP_NUM_THREADS), over host copies
+    of `n_layers` whole resident layers (3.42 GB each, so the experts come from DRAM, not cache), for about
+    `seconds`; returns GB/s with the same byte accounting as the GPU figure."""
     import numpy as np
     import torch
-    from threadpoolctl import threadpool_limits
-    from oracle import experts as ox, routing as orr, mxfp4 as oq
+    from oracle import cpu_decode as cd, mxfp4 as oq
+    threads = torch.get_num_threads()
     rng = np.random.default_rng(7)
+    host = []
+    for l in range(min(n_layers, len(layers.blocks))):     # staging, not timed
+        b = layers.blocks[l]
+        host.append(({k: v.cpu() for k, v in b.bank.items()}, torch.from_numpy(layers.W[l]),
+                     b.router.e_score_correction_bias.cpu()))
     done, t_cpu, nbytes = 0, 0.0, 0.0
-    blocks = layers.blocks
-    with threadpool_limits(1):
-        while t_cpu < seconds and done < 50:
-            l = done % len(blocks)
-            x = oq.round_bf16(steered_rows(rng, layers.W[l], controlled_sets(rng, 1)))
-            _, inds, _ = blocks[l](torch.from_numpy(x).to(torch.bfloat16).cuda(), return_routes=True)
-            sel = inds.cpu().numpy()[0]
-            b = blocks[l].bank
-            idx = torch.from_numpy(sel.astype(np.int64)).cuda()
-            sub = {k: v[idx].cpu().numpy() for k, v in b.items()}          # staging, not timed
-            sub = {k: (v.view(np.uint32) if k.endswith("_w") else v) for k, v in sub.items()}
-            t0 = time.perf_counter()
-            logits = orr.router_logits(x, layers.W[l])
-            oi, ow = orr.select_topk(logits, np.zeros(E, np.float32), K)
-            pool = ox.ExpertPool(sub)
-            remap = {int(e): j for j, e in enumerate(sel)}
-            slots = np.array([remap.get(int(e), 0) for e in oi[0]])
-            ox.gather_m1(x[0], pool, slots, ow[0])
-            t_cpu += time.perf_counter() - t0
-            done += 1
-            nbytes += len(np.unique(oi[0])) * 13369344 + ROUTER_BYTES + 2 * H * 2
-    return {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{done} one-row MoE-layer decode steps (router + 8 MXFP4 experts + combine) of the same "
-                      f"layers, numpy oracle, 1 thread, {t_cpu:.1f} s of CPU time; host has {os.cpu_count()} "
-                      f"logical CPUs ({_cpu_model()})"}
+    cd.decode_step(torch.zeros(H), host[0][1], host[0][2], host[0][0])             # warm-up, not timed
+    while t_cpu < seconds and done < 200:
+        pools, W, bias = host[done % len(host)]
+        x = torch.from_numpy(oq.round_bf16(steered_rows(rng, W.numpy(), controlled_sets(rng, 1)))[0])
+        t0 = time.perf_counter()
+        _, inds, _ = cd.decode_step(x, W, bias, pools, K)
+        t_cpu += time.perf_counter() - t0
+        done += 1
+        nbytes += len(np.unique(inds.numpy())) * 13369344 + ROUTER_BYTES + 2 * H * 2
+    return {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{done} one-row MoE-layer decode steps (router + 8 MXFP4 experts + combine) over host copies "
+                      f"of {len(host)} of the same layers, fp32 PyTorch restatement (oracle/cpu_decode.py), "
+                      f"{threads} threads, {t_cpu:.1f} s; host: {os.cpu_count()} logical CPUs ({_cpu_model()})"}
 
 
 def _cpu_model():
@@ -495,6 +549,9 @@ def main():
     if args.traffic_parse:
         traffic_parse(*args.traffic_parse)
         return
+    if args.trace_parse:
+        trace_parse(args.trace_parse)
+        return
     if args.traffic_run:
         traffic_run()
         return
@@ -519,11 +576,18 @@ def main():
     kt = kernel_times(head["_fn"], min(args.steps, 200))
     gu_ms, gu_n = kt.get("decode_gateup", (float("nan"), 0))
     achieved = head["_U"] * GATEUP_BYTES_PER_EXPERT / (gu_ms * 1e-3) / 1e9
+    bpl = head["_U"] * GATEUP_BYTES_PER_EXPERT
     roofline = {"bound": "hbm", "kernel": "decode_gateup_kernel", "achieved": achieved, "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                 "traffic": traffic_from_profiles("decode_gateup_kernel", "decode_m1"),
-                "bytes_per_launch": head["_U"] * GATEUP_BYTES_PER_EXPERT, "avg_us": gu_ms * 1e3,
-                "launches_timed": gu_n}
+                "bytes_per_launch": bpl, "avg_us": gu_ms * 1e3, "launches_timed": gu_n,
+                "avg_us_is": "live HIP events on the launch stream, from the previous kernel's end to this kernel's "
+                             "end (the dispatch gap before the kernel included); achieved and frac use it"}
+    tr = trace_from_profiles("decode_gateup_kernel:decode_m1")
+    if tr:     # the committed rocprofv3 trace of this benchmark: the kernel's own duration
+        roofline["avg_us_trace"] = tr["avg_us"]
+        roofline["after_previous_end_us_trace"] = tr.get("after_previous_end_us")
+        roofline["frac_trace"] = bpl / (tr["avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
 
     extra = {"kernel_us_decode_m1": {k: round(v[0] * 1e3, 2) for k, v in kt.items()}}
     if not args.no_extra:
