@@ -349,6 +349,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
     __syncthreads();
     run_pass(c0);
   }
+  mfma_f8f4_settle();
   float vg[4], vu[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {   // rows 4g+q (hi, g < 2) plus rows 8+4g+q (lo) of lane l + 32
@@ -555,6 +556,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
       run_pass(c0);
     }
     __builtin_amdgcn_wave_barrier();     // the staged rows and scales are read before the next item overwrites them
+    mfma_f8f4_settle();
     float dq[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) dq[q] = acc[q] + __shfl_xor(acc[q], 32, 64);   // hi rows + lo rows

@@ -298,6 +298,18 @@ __device__ __forceinline__ void wait_vm_keep() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
+// ------------------------------------------------------------------ MFMA result reads
+// The block-scaled fp8 x fp4 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 with an E4M3 A operand) runs 16 passes, but
+// the compiler pads a read of its result as if it took fewer: an epilogue that read the accumulator 12 wait
+// states after the last MFMA got values the MFMA had not finished writing (found on MI355X in a kernel whose
+// second MFMA was followed by a short epilogue).  Placed after a chain of these MFMAs and before anything reads
+// the accumulators, this waits 20 states and keeps the scheduler from moving instructions across it.
+__device__ __forceinline__ void mfma_f8f4_settle() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // ------------------------------------------------------------------ misc
 __device__ __forceinline__ uint32_t load_u8x4(const uint8_t* p) { return *(const uint32_t*)p; }
 

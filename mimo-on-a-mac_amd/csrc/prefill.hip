@@ -254,6 +254,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   // epilogue: lane (i, g) holds routes 16 chunk + 4 g + q at output column i of each tile.  Results go through
   // a per-wave LDS staging area (the ring is free once every wave has left the K loop) so that the global
   // stores are 16 bytes per lane.
+  mfma_f8f4_settle();
   __syncthreads();
   uint8_t* stg = pl + PF_STG * wave;
   if constexpr (GATEUP) {
