@@ -162,6 +162,16 @@ int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const f
                      void* stream);
 size_t mimo_moe_prefill_workspace_size(int T, int k, int n_slots, int H, int I);
 
+/* _moe_prefill with non-resident experts in a staging bank (model.py:230-271 with the staging banks of
+ * :140-143): slot ids [0, bank->n_slots) address the resident bank, ids bank->n_slots + j slot j of `stage`
+ * (same hidden / inter).  The reference runs the resident and the staged routes as two gather_qmm passes and
+ * merges their bf16 outputs in (token, k) order before the fixed-order sum (:244-271); here one dispatch over
+ * both banks writes the same bf16 route outputs, so y equals mimo_moe_prefill's on a bank holding every
+ * expert.  Workspace: mimo_moe_prefill_workspace_size(T, k, bank->n_slots + stage->n_slots, H, I). */
+int mimo_moe_prefill_staged(const uint16_t* x, int T, const int32_t* slot_inds, const float* w, int k,
+                            const mimo_bank* bank, const mimo_bank* stage, uint16_t* y, int32_t* status_out,
+                            void* ws, size_t ws_bytes, void* stream);
+
 /* Router + _moe_prefill for one chunk (model.py:303, :335-336): y bf16 [T, H]; inds_out / w_out / status_out
  * optional. */
 int mimo_moe_prefill_block(const uint16_t* x, int T, const uint16_t* Wg, const float* bias,

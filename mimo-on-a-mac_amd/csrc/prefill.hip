@@ -25,8 +25,10 @@ struct PrefillArgs {
   int wcap;
   const float* w;
   int T, k, S, H, I, P;
-  const uint32_t *gate_w, *up_w, *down_w;
-  const uint8_t *gate_s, *up_s, *down_s;
+  // slots [0, S0) address the bank's pools, slots [S0, S) the staging bank's (pool index 1, slot - S0)
+  int S0;
+  const uint32_t *gate_w[2], *up_w[2], *down_w[2];
+  const uint8_t *gate_s[2], *up_s[2], *down_s[2];
   const uint16_t* sigtab;
   uint8_t *hq_hi, *hq_lo, *hq_hs, *hq_ls;         // [P, I], [P, I/32] in sorted route order
   uint16_t* Y;                                    // [P, H] bf16 expert outputs, sorted route order
@@ -128,14 +130,16 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   }
   // B copies: block rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding chunk (slot - row / 4) & 3
   const bool up_half = GATEUP && wave >= 4;
-  const uint32_t* bw = GATEUP ? (up_half ? a.up_w : a.gate_w) : a.down_w;
-  const uint8_t* bw_base = reinterpret_cast<const uint8_t*>(bw) + ((size_t)slot * ncol + n0) * (K / 2);
+  const int pool = slot >= a.S0;                 // tile-uniform: the bank or the staging bank
+  const size_t ps = (size_t)(slot - (pool ? a.S0 : 0));
+  const uint32_t* bw = GATEUP ? (up_half ? a.up_w[pool] : a.gate_w[pool]) : a.down_w[pool];
+  const uint8_t* bw_base = reinterpret_cast<const uint8_t*>(bw) + (ps * ncol + n0) * (K / 2);
   const int brow_c = (N / 8) * wave;
   const uint32_t b_off = (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 2)) * (uint32_t)(K / 2) +
                          16u * (uint32_t)(((lane & 3) - (lane >> 4)) & 3);
   // scale copies: copy c covers epoch rows 8 (ECOP wave + c) .. + 7, eight lanes per row
-  const uint8_t* bs_base = (GATEUP ? a.gate_s : a.down_s) + ((size_t)slot * ncol + n0) * KS;
-  const uint8_t* us_base = a.up_s + ((size_t)slot * ncol + n0) * KS;
+  const uint8_t* bs_base = (GATEUP ? a.gate_s[pool] : a.down_s[pool]) + (ps * ncol + n0) * KS;
+  const uint8_t* us_base = a.up_s[pool] + (ps * ncol + n0) * KS;
   uint32_t e_off[Sh::ECOP], e_k4[Sh::ECOP];
   const uint8_t* e_src[Sh::ECOP];
 #pragma unroll
@@ -477,9 +481,11 @@ static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int 
 
 __global__ void reset_status_kernel(int32_t* status) { status[0] = 0; }
 
+// stage (optional): a second bank whose slots follow the bank's (slot ids bank->n_slots ...)
 static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* wts, int k, const mimo_bank* bank,
-                       uint16_t* y, const PrefillWs& ws, hipStream_t st, const uint16_t* resid = nullptr) {
-  const int H = bank->hidden, I = bank->inter, S = bank->n_slots;
+                       const mimo_bank* stage, uint16_t* y, const PrefillWs& ws, hipStream_t st,
+                       const uint16_t* resid = nullptr) {
+  const int H = bank->hidden, I = bank->inter, S = bank->n_slots + (stage ? stage->n_slots : 0);
   const int P = T * k;
   // the GEMM kernels address activation and h rows with 32-bit offsets
   MIMO_REQUIRE((int64_t)T * H < (int64_t)1 << 31 && (int64_t)P * I < (int64_t)1 << 31, MIMO_ERR_SHAPE,
@@ -497,8 +503,12 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   a.xq_hi = ws.xq_hi; a.xq_lo = ws.xq_lo; a.xq_hs = ws.xq_hs; a.xq_ls = ws.xq_ls;
   a.perm = ws.perm; a.offsets = ws.offsets; a.inv = ws.inv; a.w = wts; a.tiles = ws.tiles; a.wcap = tl.wcap;
   a.T = T; a.k = k; a.S = S; a.H = H; a.I = I; a.P = P;
-  a.gate_w = bank->gate_w; a.up_w = bank->up_w; a.down_w = bank->down_w;
-  a.gate_s = bank->gate_s; a.up_s = bank->up_s; a.down_s = bank->down_s;
+  a.S0 = bank->n_slots;
+  const mimo_bank* pools[2] = {bank, stage ? stage : bank};
+  for (int i = 0; i < 2; ++i) {
+    a.gate_w[i] = pools[i]->gate_w; a.up_w[i] = pools[i]->up_w; a.down_w[i] = pools[i]->down_w;
+    a.gate_s[i] = pools[i]->gate_s; a.up_s[i] = pools[i]->up_s; a.down_s[i] = pools[i]->down_s;
+  }
   a.sigtab = sig;
   a.hq_hi = ws.hq_hi; a.hq_lo = ws.hq_lo; a.hq_hs = ws.hq_hs; a.hq_ls = ws.hq_ls;
   a.Y = ws.Y; a.y = y;
@@ -568,7 +578,30 @@ int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const f
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill: workspace too small (need %zu)", c.off);
   if (status_out) pw.status = status_out;
   reset_status_kernel<<<1, 1, 0, as_stream(stream)>>>(pw.status);
-  return run_prefill(x, T, slot_inds, w, k, bank, y, pw, as_stream(stream));
+  return run_prefill(x, T, slot_inds, w, k, bank, nullptr, y, pw, as_stream(stream));
+}
+
+int mimo_moe_prefill_staged(const uint16_t* x, int T, const int32_t* slot_inds, const float* w, int k,
+                            const mimo_bank* bank, const mimo_bank* stage, uint16_t* y, int32_t* status_out, void* ws,
+                            size_t ws_bytes, void* stream) {
+  ProfChain chain;
+  int rc = check_prefill_bank(bank);
+  if (rc) return rc;
+  rc = check_prefill_bank(stage);
+  if (rc) return rc;
+  MIMO_REQUIRE(stage->hidden == bank->hidden && stage->inter == bank->inter, MIMO_ERR_SHAPE,
+               "moe_prefill_staged: staging bank of another expert shape");
+  MIMO_REQUIRE(bank->n_slots + stage->n_slots <= 1024, MIMO_ERR_SHAPE,
+               "moe_prefill_staged: at most 1024 slots in the bank and the staging bank together");
+  MIMO_REQUIRE(x && slot_inds && w && y, MIMO_ERR_ARG, "moe_prefill_staged: null pointer");
+  MIMO_REQUIRE(T >= 1 && k >= 1 && (int64_t)T * k < (1 << 30), MIMO_ERR_SHAPE, "moe_prefill_staged: bad T or k");
+  MIMO_REQUIRE(aligned16(x) && aligned16(y), MIMO_ERR_ALIGN, "moe_prefill_staged: 16-byte alignment");
+  Carve c(ws, ws_bytes);
+  PrefillWs pw = carve_prefill(c, T, k, bank->n_slots + stage->n_slots, bank->hidden, bank->inter, 0);
+  MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill_staged: workspace too small (need %zu)", c.off);
+  if (status_out) pw.status = status_out;
+  reset_status_kernel<<<1, 1, 0, as_stream(stream)>>>(pw.status);
+  return run_prefill(x, T, slot_inds, w, k, bank, stage, y, pw, as_stream(stream));
 }
 
 size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, int H, int I) {
@@ -602,7 +635,7 @@ static int prefill_block_impl(const uint16_t* x, int T, const uint16_t* Wg, cons
   rc = launch_router_select(pw.logits, bias, T, E, k, 1.0f, inds, wts, slot_of, pw.slot_inds, bank->n_slots, pw.status,
                             st);
   if (rc) return rc;
-  return run_prefill(x, T, pw.slot_inds, wts, k, bank, y, pw, st, resid);
+  return run_prefill(x, T, pw.slot_inds, wts, k, bank, nullptr, y, pw, st, resid);
 }
 }  // namespace mimo
 

@@ -9,5 +9,5 @@ from .cache import SlotCache  # noqa: F401
 from .kernels import sigmoid_table, group_routes, moe_experts  # noqa: F401
 from .model import Router, MoEBlock, select_from_logits, prefill_dispatch  # noqa: F401
 from .store import ExpertStore, load_block, load_router, write_expert_layer  # noqa: F401
-from .residency import StreamedMoEBlock  # noqa: F401
+from .residency import StagingBanks, StreamedMoEBlock  # noqa: F401
 from .layer import MoELayer, load_layer, load_norm, layernorm_epsilon  # noqa: F401

@@ -53,6 +53,7 @@ SIGNATURES = {
     "mimo_moe_decode_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "mimo_moe_prefill": (I32, [P, I32, P, P, I32, BANKP, P, P, P, SZ, P]),
     "mimo_moe_prefill_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
+    "mimo_moe_prefill_staged": (I32, [P, I32, P, P, I32, BANKP, BANKP, P, P, P, SZ, P]),
     "mimo_moe_prefill_block": (I32, [P, I32, P, P, P, I32, I32, BANKP, P, P, P, P, P, SZ, P]),
     "mimo_moe_prefill_block_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "mimo_rmsnorm": (I32, [P, I32, I32, P, F32, P, P]),

@@ -124,6 +124,13 @@ class MoELayer:
             return self.block.prefetch(experts)
         return 0
 
+    def prefetch_stage(self):
+        """Before a long prefill chunk reaches this layer (model.py:273-285, :336-339): a streamed block streams
+        all its non-resident experts into the next shared staging bank.  Returns the number of experts read."""
+        if isinstance(self.block, StreamedMoEBlock):
+            return self.block.prefetch_stage()
+        return 0
+
 
 def norm_name(L):
     return f"model.layers.{L}.post_attention_layernorm.weight"

@@ -77,3 +77,32 @@ def test_prefill_block_router_and_decode_consistency(rng, full_pool):
         assert torch.equal(it[0], inds[t])
         torch.testing.assert_close(wt[0], w[t], rtol=1e-5, atol=1e-7)
         assert_bf16_close(bf16_np(y[t]), bf16_np(yt[0]), what=f"decode vs prefill token {t}")
+
+
+@pytest.mark.parametrize("S0", [1, 100, 255])
+def test_prefill_staged_split_bank_equals_one_bank(rng, full_pool, S0):
+    """mimo_moe_prefill_staged over a bank of the first S0 slots and a staging bank of the rest (slot ids
+    unchanged) gives mimo_moe_prefill's y on the whole bank bit for bit: the tiles of slots below S0 read the
+    first bank, the others the second at slot - S0, including a tile whose slot is the first staged one."""
+    from mimo_stream import _lib, pools
+    T, k, H, I = 1024, 8, 4096, 2048
+    x = to_dev_bf16(rand_bf16(rng, (T, H)))
+    inds = torch.from_numpy(zipf_routes(rng, T, 256, k)).cuda()
+    w = torch.from_numpy(rng.random((T, k)).astype(np.float32)).cuda()
+    want = _block(rng, full_pool, H, 256, k)._moe_prefill(x, inds, w)
+    first = {n: t[:S0] for n, t in full_pool.items()}
+    rest = {n: t[S0:] for n, t in full_pool.items()}
+    y = torch.empty_like(want)
+    status = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    nb = _lib.load().mimo_moe_prefill_workspace_size(T, k, 256, H, I)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    _lib.call("mimo_moe_prefill_staged", _lib.ptr(x), T, _lib.ptr(inds), _lib.ptr(w), k, pools.bank_struct(first),
+              pools.bank_struct(rest), _lib.ptr(y), _lib.ptr(status), _lib.ptr(ws), nb, _lib.stream_ptr())
+    assert int(status.item()) == 0
+    assert torch.equal(y, want)
+    # a slot id past both banks is flagged
+    bad = inds.clone()
+    bad[3, 2] = 256
+    _lib.call("mimo_moe_prefill_staged", _lib.ptr(x), T, _lib.ptr(bad), _lib.ptr(w), k, pools.bank_struct(first),
+              pools.bank_struct(rest), _lib.ptr(y), _lib.ptr(status), _lib.ptr(ws), nb, _lib.stream_ptr())
+    assert int(status.item()) != 0
