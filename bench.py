@@ -9,10 +9,12 @@ MoE-layer decode (router -> top-8 -> grouping -> experts -> combine) on a freshl
 of a HIP graph holding exactly --steps steps, inputs resident in HBM.
 
 Also reported (field "extra"): decode at 2, 4, 8 rows with controlled routing (consecutive rows share ~2.6
-of 8 experts), prefill at 512 / 2048 tokens with Zipf(1.1) expert popularity, a 48-layer stack decode at 1
-and 4 rows, the MoE half of a decoder layer (post-attention RMSNorm + block + residual) against the block alone
-at 1 row and 2048 tokens, and the per-kernel durations measured with HIP events.  "cpu_baseline" times the numpy oracle
-(the CPU restatement of the reference algorithm) on a bounded sample of the same workload.
+of 8 experts), prefill at 512 / 2048 tokens with Zipf(1.1) expert popularity and at 2048 tokens with every route
+on 16 popular experts (the GEMMs' compute-bound tiles on their own), a 48-layer stack decode at 1 and 4 rows,
+the MoE half of a decoder layer (post-attention RMSNorm + block + residual) against the block alone at 1 row and
+2048 tokens, and the per-kernel durations measured with HIP events.  "cpu_baseline" times an fp32 PyTorch CPU
+restatement of the one-row decode (oracle/cpu_decode.py) on every host thread, on a bounded sample of the same
+workload.
 
     python bench.py [--gpus 1] [--steps 500] [--warmup 20]
 
@@ -38,6 +40,9 @@ H, I, E, K = 4096, 2048, 256, 8
 ROUTER_BYTES = E * H * 2
 GATEUP_BYTES_PER_EXPERT = 2 * (I * H // 2 + I * H // 32)      # 8,912,896
 FLOPS_PER_ROUTE = 2 * (2 * I * H + H * I)                      # 50,331,648
+PF_HOT_EXPERTS = 16          # concentrated prefill: every token's 8 experts among 16 (1,024 routes each at 2048)
+HILO_CEILING_TFLOPS = 2500.0  # useful flops when each product takes two fp8 x fp4 MFMAs at the 5.0 PF fp8 peak
+ISSUE_RATE_TFLOPS = 3310.0    # issued fp8 x fp4 MFMA flops at the rate a throughput probe measured (48.6 cycles)
 
 
 def log(*a):
@@ -64,6 +69,9 @@ def parse():
                          "SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE, using the kernel durations of a "
                          "--kernel-trace run of the same payload (second argument)")
     ap.add_argument("--mfma-trace", metavar="TRACE_DIR", help="kernel-trace directory for --mfma-parse")
+    ap.add_argument("--pipe-parse", nargs=2, metavar=("LDS_DIR", "WAIT_DIR"),
+                    help="summarise two rocprofv3 --pmc runs of --traffic-run (LDS counters, then wave wait and "
+                         "issue counters) for the prefill GEMMs")
     ap.add_argument("--trace-parse", metavar="TRACE_DIR",
                     help="summarise a rocprofv3 --kernel-trace run of this benchmark: a markdown table per kernel "
                          "and grid on stdout, and the headline kernel's average duration (and its interval from "
@@ -203,15 +211,31 @@ def zipf_routes(T, seed, nin):
     return out
 
 
-def prefill_case(layers, T, steps, warmup, seed, device, timed=True):
-    """Expert path of prefill (dispatch + grouped GEMMs + combine) with Zipf(1.1) routes, layers rotated.
-    With timed=False only the step function and the routing statistics are returned."""
+def hot_routes(T, seed, nin, n_hot=PF_HOT_EXPERTS):
+    """`nin` routings of T tokens concentrated on `n_hot` experts (a seeded subset): each token takes 8 of them
+    uniformly at random, so every expert gets about T * 8 / n_hot routes and every row tile is a full wide tile
+    of a popular expert (the compute-bound part of a Zipf prefill, measured on its own)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    hot = rng.permutation(E)[:n_hot]
+    out = []
+    for _ in range(nin):
+        pick = np.argsort(rng.random((T, n_hot)), axis=1)[:, :K]
+        w = rng.random((T, K)).astype(np.float32)
+        w /= w.sum(1, keepdims=True)
+        out.append((hot[pick].astype(np.int32), w))
+    return out
+
+
+def prefill_case(layers, T, steps, warmup, seed, device, timed=True, routes=None):
+    """Expert path of prefill (dispatch + grouped GEMMs + combine) with Zipf(1.1) routes (or the given routings),
+    layers rotated.  With timed=False only the step function and the routing statistics are returned."""
     import numpy as np
     import torch
     n = min(len(layers.blocks), 8)
     nin = 4
     Xs, Is, Ws, Us = [], [], [], []
-    for inds, w in zipf_routes(T, seed, nin):
+    for inds, w in (routes if routes is not None else zipf_routes(T, seed, nin)):
         Xs.append(torch.randn(T, H, device=device).to(torch.bfloat16))
         Is.append(torch.from_numpy(inds).to(device))
         Ws.append(torch.from_numpy(w).to(device))
@@ -231,6 +255,26 @@ def prefill_case(layers, T, steps, warmup, seed, device, timed=True):
             "GBps": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "TFLOPs": flops / (ms * 1e-3) / 1e12,
             "mxfp4_mfma_frac": flops / (ms * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS, "_fn": fn}
+
+
+def hot_prefill_case(layers, T, device):
+    """Prefill with every route on PF_HOT_EXPERTS experts (hot_routes): only full wide tiles of popular experts,
+    the GEMMs' compute-bound case.  Per GEMM: useful TFLOP/s (one product = 2 flops per multiply-add), against
+    the hi/lo ceiling (2 fp8 x fp4 MFMAs per product at the 5.0 PF fp8 peak) and, as issued MFMA flops (hi + lo),
+    against the issue rate a throughput probe of the same instruction measured."""
+    r = prefill_case(layers, T, 20, 3, seed=0, device=device, routes=hot_routes(T, 60 + T, 4))
+    kt = kernel_times(r.pop("_fn"), 4)
+    r["kernel_us"] = {k: round(v[0] * 1e3, 1) for k, v in kt.items()}
+    r["hot_experts"] = PF_HOT_EXPERTS
+    r["routes_per_expert"] = T * K / PF_HOT_EXPERTS
+    for tag, kern, flops in (("gateup", "prefill_gateup", T * K * 2 * (2 * I * H)),
+                             ("down", "prefill_down", T * K * 2 * (H * I))):
+        us = kt[kern][0] * 1e3
+        useful = flops / (us * 1e-6) / 1e12
+        r[tag] = {"us": round(us, 1), "useful_TFLOPs": useful, "hilo_ceiling_frac": useful / HILO_CEILING_TFLOPS,
+                  "issued_vs_probe_rate": 2 * useful / ISSUE_RATE_TFLOPS,
+                  "mxfp4_mfma_frac": useful / MXFP4_PEAK_TFLOPS}
+    return r
 
 
 def stack_case(layers, M, tokens, device, seed):
@@ -372,6 +416,7 @@ def _cpu_model():
 
 
 CALIB_BYTES = 1 << 30        # the calibration copy reads and writes this many bytes
+PF_HOT_STEPS = 4             # prefill layers with routes concentrated on PF_HOT_EXPERTS experts
 
 
 PF_TRAFFIC_T = 2048
@@ -381,7 +426,8 @@ PF_TRAFFIC_STEPS = 8
 def traffic_run():
     """Workload for the counter runs: the calibration copy (an elementwise multiply by one over 1 GiB, so a
     kernel, not a DMA copy), then 24 one-row decode steps rotating over 8 resident layers (8 x 103 MB, more
-    than the 256 MB MALL holds), then 8 prefill layers of 2048 tokens with Zipf(1.1) routes, one per layer."""
+    than the 256 MB MALL holds), then 8 prefill layers of 2048 tokens with Zipf(1.1) routes, one per layer, then 4
+    prefill layers of 2048 tokens with every route on 16 popular experts (hot_routes)."""
     import numpy as np
     import torch
     src = torch.ones(CALIB_BYTES // 2, dtype=torch.bfloat16, device="cuda")
@@ -399,6 +445,11 @@ def traffic_run():
     torch.cuda.synchronize()
     r = prefill_case(layers, PF_TRAFFIC_T, 0, 0, seed=20 + PF_TRAFFIC_T, device="cuda", timed=False)
     for s in range(PF_TRAFFIC_STEPS):
+        r["_fn"](s)
+    torch.cuda.synchronize()
+    r = prefill_case(layers, PF_TRAFFIC_T, 0, 0, seed=0, device="cuda", timed=False,
+                     routes=hot_routes(PF_TRAFFIC_T, 60 + PF_TRAFFIC_T, 4))
+    for s in range(PF_HOT_STEPS):
         r["_fn"](s)
     torch.cuda.synchronize()
     log("[traffic] done")
@@ -419,9 +470,9 @@ def _counter_rows(d):
 def traffic_parse(fetch_dir, write_dir):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) averaged per kernel; each scaled by bytes / counter of the
     calibration copy.  Writes profiles/traffic.json and prints a markdown summary."""
-    def per_kernel(d, counter):
+    def per_kernel(d, counter):   # per kernel, values in dispatch order
         acc = {}
-        for r in _counter_rows(d):
+        for r in sorted(_counter_rows(d), key=lambda r: int(r["Dispatch_Id"])):
             if r.get("Counter_Name") != counter:
                 continue
             acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) * 1024.0)
@@ -463,6 +514,7 @@ def traffic_parse(fetch_dir, write_dir):
         key = lambda n, g=gate: f"prefill_gemm_kernel<{'true' if g else 'false'}>" in n
         pname, pf_ = pick(f, key)
         _, pw_ = pick(w, key)
+        pf_, pw_ = pf_[:PF_TRAFFIC_STEPS], pw_[:PF_TRAFFIC_STEPS]     # the Zipf layers come first
         pfetch = sum(pf_) / len(pf_) * fetch_scale
         pwrite = sum(pw_) / len(pw_) * write_scale
         tag = "prefill_gateup" if gate else "prefill_down"
@@ -485,35 +537,74 @@ def traffic_parse(fetch_dir, write_dir):
 
 def mfma_parse(pmc_dir, trace_dir):
     """MFMA work of the prefill GEMMs from a --pmc run (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES,
-    GRBM_GUI_ACTIVE) and their durations from a --kernel-trace run of the same payload."""
+    GRBM_GUI_ACTIVE) and their durations from a --kernel-trace run of the same payload: the Zipf(1.1) layers
+    (the first PF_TRAFFIC_STEPS dispatches of each GEMM) and the layers on PF_HOT_EXPERTS experts (the next
+    PF_HOT_STEPS)."""
     import csv
     import glob
     cnt = {}
-    for r in _counter_rows(pmc_dir):
+    for r in sorted(_counter_rows(pmc_dir), key=lambda r: int(r["Dispatch_Id"])):
         k = r["Kernel_Name"]
         if "prefill_gemm_kernel" not in k:
             continue
         cnt.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
     dur = {}
+    rows = []
     for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
         with open(path) as f:
-            for r in csv.DictReader(f):
-                if "prefill_gemm_kernel" in r["Kernel_Name"]:
-                    dur.setdefault(r["Kernel_Name"], []).append(
-                        (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
-    print("| kernel | dispatches | MFMA instr / launch | avg µs | MFMA TFLOP/s issued (hi + lo) | "
-          "useful TFLOP/s | busy cycles / instr | GRBM cycles / µs |")
-    print("|---|---|---|---|---|---|---|---|")
+            rows += [r for r in csv.DictReader(f) if "prefill_gemm_kernel" in r["Kernel_Name"]]
+    for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
+        dur.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
+    groups = ((f"2048 tokens, Zipf(1.1)", 0, PF_TRAFFIC_STEPS),
+              (f"2048 tokens on {PF_HOT_EXPERTS} experts", PF_TRAFFIC_STEPS, PF_TRAFFIC_STEPS + PF_HOT_STEPS))
+    print("| kernel | routes | dispatches | MFMA instr / launch | avg µs | MFMA TFLOP/s issued (hi + lo) | "
+          "useful TFLOP/s | issued / probe rate | useful / hi-lo ceiling | busy cycles / instr | GRBM cycles / µs |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
     for k in sorted(cnt):
-        c = cnt[k]
-        n = len(c["SQ_INSTS_MFMA"])
-        inst = sum(c["SQ_INSTS_MFMA"]) / n
-        busy = sum(c["SQ_VALU_MFMA_BUSY_CYCLES"]) / n
-        grbm = sum(c["GRBM_GUI_ACTIVE"]) / n
-        d = sum(dur.get(k, [float("nan")])) / max(1, len(dur.get(k, [])))
-        issued = inst * 16 * 16 * 128 * 2 / d / 1e12
-        print(f"| {k.split('(')[0].replace('void mimo::', '')} | {n} | {inst:,.0f} | {d * 1e6:.1f} | "
-              f"{issued:.0f} | {issued / 2:.0f} | {busy / inst:.1f} | {grbm / (d * 1e6):.0f} |")
+        for label, a, b in groups:
+            c = {n: v[a:b] for n, v in cnt[k].items()}
+            dd = dur.get(k, [])[a:b]
+            n = len(c["SQ_INSTS_MFMA"])
+            if not n or not dd:
+                continue
+            inst = sum(c["SQ_INSTS_MFMA"]) / n
+            busy = sum(c["SQ_VALU_MFMA_BUSY_CYCLES"]) / n
+            grbm = sum(c["GRBM_GUI_ACTIVE"]) / n
+            d = sum(dd) / len(dd)
+            issued = inst * 16 * 16 * 128 * 2 / d / 1e12
+            print(f"| {k.split('(')[0].replace('void mimo::', '')} | {label} | {n} | {inst:,.0f} | {d * 1e6:.1f} | "
+                  f"{issued:.0f} | {issued / 2:.0f} | {issued / ISSUE_RATE_TFLOPS:.2f} | "
+                  f"{issued / 2 / HILO_CEILING_TFLOPS:.2f} | {busy / inst:.1f} | {grbm / (d * 1e6):.0f} |")
+
+
+def pipe_parse(lds_dir, wait_dir):
+    """Where the prefill GEMMs' waves spend their cycles, per kernel and routing group (as mfma_parse):
+    LDS utilisation (SQ_LDS_IDX_ACTIVE over GRBM_GUI_ACTIVE of one XCD x 256 CUs), bank conflicts per access,
+    MFMA pipe busy per SIMD, and the fractions of wave-cycles waiting (SQ_WAIT_ANY: s_waitcnt and barriers;
+    SQ_WAIT_INST_ANY: an instruction waiting to issue) or issuing (SQ_ACTIVE_INST_ANY / _LDS)."""
+    def load(d):
+        cnt = {}
+        for r in sorted(_counter_rows(d), key=lambda r: int(r["Dispatch_Id"])):
+            if "prefill_gemm_kernel" in r["Kernel_Name"]:
+                cnt.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        return cnt
+    lds, wt = load(lds_dir), load(wait_dir)
+    groups = ((f"2048 tokens, Zipf(1.1)", 0, PF_TRAFFIC_STEPS),
+              (f"2048 tokens on {PF_HOT_EXPERTS} experts", PF_TRAFFIC_STEPS, PF_TRAFFIC_STEPS + PF_HOT_STEPS))
+    print("| kernel | routes | LDS busy | bank conflicts / access | MFMA busy / SIMD | waiting (waitcnt, barrier) | "
+          "waiting to issue | issuing | issuing LDS |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for k in sorted(lds):
+        for label, a, b in groups:
+            m = lambda c, src: sum(src[k][c][a:b]) / len(src[k][c][a:b])
+            grbm = m("GRBM_GUI_ACTIVE", lds) / 8          # summed over the 8 XCDs
+            ia, bc = m("SQ_LDS_IDX_ACTIVE", lds), m("SQ_LDS_BANK_CONFLICT", lds)
+            g2 = m("GRBM_GUI_ACTIVE", wt) / 8
+            wc = m("SQ_WAVE_CYCLES", wt)
+            print(f"| {k.split('(')[0].replace('void mimo::', '')} | {label} | {ia / (grbm * 256):.2f} | {bc / (ia - bc):.2f} | "
+                  f"{m('SQ_VALU_MFMA_BUSY_CYCLES', wt) / (g2 * 1024):.2f} | {m('SQ_WAIT_ANY', wt) / wc:.2f} | "
+                  f"{m('SQ_WAIT_INST_ANY', wt) / wc:.2f} | {m('SQ_ACTIVE_INST_ANY', wt) / wc:.2f} | "
+                  f"{m('SQ_ACTIVE_INST_LDS', wt) / wc:.2f} |")
 
 
 def layer_case(layers, T, steps, warmup, seed, device):
@@ -545,6 +636,9 @@ def main():
     args = parse()
     if args.mfma_parse:
         mfma_parse(args.mfma_parse, args.mfma_trace)
+        return
+    if args.pipe_parse:
+        pipe_parse(*args.pipe_parse)
         return
     if args.traffic_parse:
         traffic_parse(*args.traffic_parse)
@@ -608,6 +702,13 @@ def main():
                 log(f"[bench] prefill T={T}: {r['ms_per_layer']:.3f} ms/layer, {r['tokens_per_s']:.0f} tok/s")
             except Exception as e:
                 extra[f"prefill_t{T}"] = {"error": repr(e)}
+        key = f"prefill_t2048_hot{PF_HOT_EXPERTS}"
+        try:
+            extra[key] = hot_prefill_case(layers, 2048, device)
+            log(f"[bench] prefill T=2048 on {PF_HOT_EXPERTS} experts: {extra[key]['ms_per_layer']:.3f} ms/layer, "
+                f"gate/up {extra[key]['gateup']['useful_TFLOPs']:.0f} useful TFLOP/s")
+        except Exception as e:
+            extra[key] = {"error": repr(e)}
         for M in (1, 4):
             try:
                 r = stack_case(layers, M, tokens=4, device=device, seed=30 + M)
