@@ -467,6 +467,22 @@ def _counter_rows(d):
     return rows
 
 
+def gemm_kernels(gate):
+    """Kernel-name tests for the two launches of one prefill GEMM: (narrow tiles, wide tiles)."""
+    g = "true" if gate else "false"
+    return (lambda n: f"prefill_gemm_kernel<{g}, false>" in n), (lambda n: f"prefill_gemm_kernel<{g}, true>" in n)
+
+
+def per_layer(vals_narrow, vals_wide, combine=lambda a, b: a + b):
+    """One value per prefill layer from the per-dispatch values of its narrow and wide launches (dispatch
+    order; a layer without narrow tiles has no narrow launch only when no layer has one)."""
+    if not vals_narrow:
+        return list(vals_wide)
+    if len(vals_narrow) != len(vals_wide):
+        raise SystemExit(f"{len(vals_narrow)} narrow vs {len(vals_wide)} wide launches")
+    return [combine(a, b) for a, b in zip(vals_narrow, vals_wide)]
+
+
 def traffic_parse(fetch_dir, write_dir):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) averaged per kernel; each scaled by bytes / counter of the
     calibration copy.  Writes profiles/traffic.json and prints a markdown summary."""
@@ -510,11 +526,15 @@ def traffic_parse(fetch_dir, write_dir):
     split = lambda rows_, cols: 2 * rows_ * cols + 2 * rows_ * cols // 32          # hi + lo codes and scales
     algo_pf = {True: U * GATEUP_BYTES_PER_EXPERT + split(T, H) + split(P, I),
                False: U * (H * I // 2 + H * I // 32) + split(P, I) + P * H * 2}
+    def layer_vals(acc, gate):
+        kn, kw = gemm_kernels(gate)
+        vn = [v for n in acc if kn(n) for v in acc[n]]
+        _, vw = pick(acc, kw)
+        return per_layer(vn, vw)
     for gate in (True, False):
-        key = lambda n, g=gate: f"prefill_gemm_kernel<{'true' if g else 'false'}>" in n
-        pname, pf_ = pick(f, key)
-        _, pw_ = pick(w, key)
-        pf_, pw_ = pf_[:PF_TRAFFIC_STEPS], pw_[:PF_TRAFFIC_STEPS]     # the Zipf layers come first
+        pname = f"prefill_gemm_kernel<{'true' if gate else 'false'}, narrow + wide>"
+        pf_ = layer_vals(f, gate)[:PF_TRAFFIC_STEPS]                  # the Zipf layers come first
+        pw_ = layer_vals(w, gate)[:PF_TRAFFIC_STEPS]
         pfetch = sum(pf_) / len(pf_) * fetch_scale
         pwrite = sum(pw_) / len(pw_) * write_scale
         tag = "prefill_gateup" if gate else "prefill_down"
@@ -538,47 +558,50 @@ def traffic_parse(fetch_dir, write_dir):
 def mfma_parse(pmc_dir, trace_dir):
     """MFMA work of the prefill GEMMs from a --pmc run (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES,
     GRBM_GUI_ACTIVE) and their durations from a --kernel-trace run of the same payload: the Zipf(1.1) layers
-    (the first PF_TRAFFIC_STEPS dispatches of each GEMM) and the layers on PF_HOT_EXPERTS experts (the next
-    PF_HOT_STEPS)."""
+    (the first PF_TRAFFIC_STEPS of each GEMM) and the layers on PF_HOT_EXPERTS experts (the next PF_HOT_STEPS).
+    A GEMM is two concurrent launches (narrow and wide tiles): instructions are summed, its time runs from the
+    first start to the last end of the pair in the trace run."""
     import csv
     import glob
     cnt = {}
     for r in sorted(_counter_rows(pmc_dir), key=lambda r: int(r["Dispatch_Id"])):
         k = r["Kernel_Name"]
-        if "prefill_gemm_kernel" not in k:
-            continue
-        cnt.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
-    dur = {}
-    rows = []
+        if "prefill_gemm_kernel" in k:
+            cnt.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    spans = {}
+    trows = []
     for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
         with open(path) as f:
-            rows += [r for r in csv.DictReader(f) if "prefill_gemm_kernel" in r["Kernel_Name"]]
-    for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
-        dur.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
+            trows += [r for r in csv.DictReader(f) if "prefill_gemm_kernel" in r["Kernel_Name"]]
+    for r in sorted(trows, key=lambda r: int(r["Dispatch_Id"])):
+        spans.setdefault(r["Kernel_Name"], []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     groups = ((f"2048 tokens, Zipf(1.1)", 0, PF_TRAFFIC_STEPS),
               (f"2048 tokens on {PF_HOT_EXPERTS} experts", PF_TRAFFIC_STEPS, PF_TRAFFIC_STEPS + PF_HOT_STEPS))
-    print("| kernel | routes | dispatches | MFMA instr / launch | avg µs | MFMA TFLOP/s issued (hi + lo) | "
-          "useful TFLOP/s | issued / probe rate | useful / hi-lo ceiling | busy cycles / instr | GRBM cycles / µs |")
-    print("|---|---|---|---|---|---|---|---|---|---|---|")
-    for k in sorted(cnt):
+    print("| GEMM | routes | layers | MFMA instr / layer | avg µs | MFMA TFLOP/s issued (hi + lo) | "
+          "useful TFLOP/s | issued / probe rate | useful / hi-lo ceiling | busy cycles / instr |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for gate in (True, False):
+        kn, kw = gemm_kernels(gate)
+        sel = lambda src, key, c=None: [v for n in src if key(n) for v in (src[n][c] if c else src[n])]
+        inst = per_layer(sel(cnt, kn, "SQ_INSTS_MFMA"), sel(cnt, kw, "SQ_INSTS_MFMA"))
+        busy = per_layer(sel(cnt, kn, "SQ_VALU_MFMA_BUSY_CYCLES"), sel(cnt, kw, "SQ_VALU_MFMA_BUSY_CYCLES"))
+        span = per_layer(sel(spans, kn), sel(spans, kw), lambda a, b: (min(a[0], b[0]), max(a[1], b[1])))
         for label, a, b in groups:
-            c = {n: v[a:b] for n, v in cnt[k].items()}
-            dd = dur.get(k, [])[a:b]
-            n = len(c["SQ_INSTS_MFMA"])
-            if not n or not dd:
+            n = len(inst[a:b])
+            if not n or not span[a:b]:
                 continue
-            inst = sum(c["SQ_INSTS_MFMA"]) / n
-            busy = sum(c["SQ_VALU_MFMA_BUSY_CYCLES"]) / n
-            grbm = sum(c["GRBM_GUI_ACTIVE"]) / n
-            d = sum(dd) / len(dd)
-            issued = inst * 16 * 16 * 128 * 2 / d / 1e12
-            print(f"| {k.split('(')[0].replace('void mimo::', '')} | {label} | {n} | {inst:,.0f} | {d * 1e6:.1f} | "
-                  f"{issued:.0f} | {issued / 2:.0f} | {issued / ISSUE_RATE_TFLOPS:.2f} | "
-                  f"{issued / 2 / HILO_CEILING_TFLOPS:.2f} | {busy / inst:.1f} | {grbm / (d * 1e6):.0f} |")
+            ins = sum(inst[a:b]) / n
+            bz = sum(busy[a:b]) / n
+            d = sum((e - st) * 1e-9 for st, e in span[a:b]) / len(span[a:b])
+            issued = ins * 16 * 16 * 128 * 2 / d / 1e12
+            print(f"| {'gate/up' if gate else 'down'} | {label} | {n} | {ins:,.0f} | {d * 1e6:.1f} | {issued:.0f} | "
+                  f"{issued / 2:.0f} | {issued / ISSUE_RATE_TFLOPS:.2f} | {issued / 2 / HILO_CEILING_TFLOPS:.2f} | "
+                  f"{bz / ins:.1f} |")
 
 
 def pipe_parse(lds_dir, wait_dir):
-    """Where the prefill GEMMs' waves spend their cycles, per kernel and routing group (as mfma_parse):
+    """Where the prefill GEMMs' waves spend their cycles, per launch (narrow or wide tiles; counter runs serialise
+    the two launches of a GEMM) and routing group (as mfma_parse):
     LDS utilisation (SQ_LDS_IDX_ACTIVE over GRBM_GUI_ACTIVE of one XCD x 256 CUs), bank conflicts per access,
     MFMA pipe busy per SIMD, and the fractions of wave-cycles waiting (SQ_WAIT_ANY: s_waitcnt and barriers;
     SQ_WAIT_INST_ANY: an instruction waiting to issue) or issuing (SQ_ACTIVE_INST_ANY / _LDS)."""
@@ -601,6 +624,8 @@ def pipe_parse(lds_dir, wait_dir):
             ia, bc = m("SQ_LDS_IDX_ACTIVE", lds), m("SQ_LDS_BANK_CONFLICT", lds)
             g2 = m("GRBM_GUI_ACTIVE", wt) / 8
             wc = m("SQ_WAVE_CYCLES", wt)
+            if ia <= bc or wc <= 0:                      # a launch with no tiles of its shape in these layers
+                continue
             print(f"| {k.split('(')[0].replace('void mimo::', '')} | {label} | {ia / (grbm * 256):.2f} | {bc / (ia - bc):.2f} | "
                   f"{m('SQ_VALU_MFMA_BUSY_CYCLES', wt) / (g2 * 1024):.2f} | {m('SQ_WAIT_ANY', wt) / wc:.2f} | "
                   f"{m('SQ_WAIT_INST_ANY', wt) / wc:.2f} | {m('SQ_ACTIVE_INST_ANY', wt) / wc:.2f} | "

@@ -5,12 +5,17 @@
 // gather_qmm calls, bf16 SwiGLU intermediate, bf16 expert outputs, inverse permutation, (Y.f32 * w).sum(1)).
 //
 // Tiling: the dispatch cuts each slot's sorted routes into row tiles (narrow: a slot of at most 32 routes;
-// wide: up to 96 routes) and writes the tile table.  A block (8 waves) owns one row tile and one block of
-// weight rows (narrow 512, wide 256; gate/up blocks take half of their rows from each projection).  The K
-// loop runs in steps of 128 through a 3-slot LDS ring filled by global_load_lds (activation hi and lo E4M3
-// planes of the tile's routes, the block's E2M1 weight rows; E8M0 scales once per 8 steps); each wave
+// wide: up to 64 routes) and writes the tile table.  A block (8 waves) owns one row tile and one block of
+// weight rows (narrow 512, wide 256; gate/up blocks take half of their rows from each projection).  Each GEMM
+// is two launches that run concurrently: the narrow tiles (HBM-bound) on a side stream, one workgroup per CU
+// with a 3-slot LDS ring, and the wide tiles (MFMA work of popular experts) on the caller's stream, two
+// workgroups per CU with a 2-slot ring, so one workgroup's MFMAs run while the other waits at its barrier.
+// The K loop runs in steps of 128 through the ring, filled by global_load_lds (activation hi and lo E4M3 planes
+// of the tile's routes, the block's E2M1 weight rows; E8M0 scales once per epoch of steps); each wave
 // multiplies 16-route chunks by four 16-row weight tiles, the hi and lo planes accumulating into the same
 // tile.  The epilogue stages results in LDS and writes 16-byte pieces.
+#include <mutex>
+
 #include "device.h"
 #include "host.h"
 #include "layer.h"
@@ -38,53 +43,65 @@ struct PrefillArgs {
 // Row tiles.  The dispatch cuts each slot's sorted routes into tiles of one of two shapes:
 //   narrow: a slot with at most 32 routes (2 chunks of 16) is one tile, multiplied by 512 weight rows per block
 //           (gate/up: 256 outputs of each projection; down: 512 outputs).  These blocks stream weights at the
-//           HBM rate with little MFMA work, so the wider weight tile halves their activation re-reads.
-//   wide:   a larger slot is split into ceil(count / 96) tiles of near-equal whole 16-route chunks (at most 6),
-//           multiplied by 256 weight rows per block (128 + 128 outputs, or 256 down outputs).
+//           HBM rate with little MFMA work, so the wider weight tile halves their activation re-reads.  40 KB
+//           per K-step through a 3-slot ring (two steps in flight); 160 KB of LDS, one workgroup per CU.
+//   wide:   a larger slot is split into ceil(count / 64) tiles of near-equal whole 16-route chunks (at most 4),
+//           multiplied by 256 weight rows per block (128 + 128 outputs, or 256 down outputs).  32 KB per
+//           K-step through a 2-slot ring; 77 KB of LDS, two workgroups per CU.
 // An MFMA multiplies 16 routes of one activation plane by 16 weight rows; the hi and lo planes accumulate into
 // the same tile, so each accumulator lane holds finished sums for 4 routes.
-// Both shapes stage 40 KB per K-step of 128 through a 3-slot LDS ring: the hi and lo activation code planes of
-// the tile's routes and the block's E2M1 weight rows.  The E8M0 scales of 8 K-steps (32 bytes per row) are
-// copied at once into one of two epoch buffers, one 4-byte word per lane, so scale traffic costs one request
-// per row every 8 steps.
+// The E8M0 scales of an epoch of K-steps (narrow 8 steps, 32 bytes per row; wide 4 steps, 16 bytes) are copied
+// at once into one of two epoch buffers, one 4-byte word per lane, so scale traffic costs one request per row
+// per epoch.
 constexpr int PF_NARROW_MAX = 32;
-constexpr int PF_WIDE_ROWS = 96;
+constexpr int PF_WIDE_ROWS = 64;
 constexpr int PF_UNIT = 16;                          // routes per MFMA chunk
-constexpr int PF_STAGES = 3;                         // one step multiplied while two are in flight
-constexpr int PF_STAGE = 41216;
-constexpr int PF_EPOCH = 8;                          // K-steps per scale copy
-constexpr int PF_SC = PF_STAGES * PF_STAGE;          // the two epoch buffers follow the ring
-constexpr int PF_SC_BYTES = 18432;                   // 576 rows x 32 bytes (narrow: 64 A rows + 512 B rows)
-constexpr int PF_LDS = PF_SC + 2 * PF_SC_BYTES;      // 160512 bytes
 
 // Stage layout: A planes of R routes x 128 codes, the 16-byte chunk q of route r at slot q ^ (r & 7), the lo
 // plane 128 bytes off the hi plane's bank phase; B rows of 64 bytes, chunk g of row r at slot (g + (r & 15) / 4)
-// & 3.  Both make the MFMA operand reads conflict-free.  Copies per wave: ACOP + BCOP per K-step (5 in both
-// shapes, one per 8-route block of a plane or 16 weight rows), ECOP per epoch.  A wave multiplies 4 weight
-// tiles (64 rows) by NJ 16-route chunks spaced CSTEP apart.
+// & 3.  Both make the MFMA operand reads conflict-free.  Copies per wave: ACOP + BCOP per K-step (one per
+// 8-route block of a plane or 16 weight rows), up to ECOP of the NCOPY epoch copies per epoch.  A wave
+// multiplies 4 weight tiles (64 rows) by NJ 16-route chunks spaced CSTEP apart; TGW waves cover the N rows.
+// The ring holds STAGES steps of STAGE bytes, then two epoch buffers of SC_ROWS rows (2R + N used); STG bytes
+// per wave stage the outputs after the K loop.
 template <bool WIDE> struct PfShape;
 template <> struct PfShape<false> {
   static constexpr int R = 32, CB = 4, N = 512, A_PL = 4224, B_OFF = 8448;
-  static constexpr int ACOP = 1, BCOP = 4, ECOP = 9, NJ = 2, CSTEP = 1;
+  static constexpr int ACOP = 1, BCOP = 4, NCOPY = 72, ECOP = 9, NJ = 2, CSTEP = 1, TGW = 8;
+  static constexpr int STAGES = 3, STAGE = 41216, EPOCH = 8, SC_ROWS = 576, STG = 6144, BLOCKS_PER_CU = 1;
 };
 template <> struct PfShape<true> {
-  static constexpr int R = 96, CB = 12, N = 256, A_PL = 12416, B_OFF = 24832;
-  static constexpr int ACOP = 3, BCOP = 2, ECOP = 7, NJ = 3, CSTEP = 2;
+  static constexpr int R = 64, CB = 8, N = 256, A_PL = 8320, B_OFF = 16640;
+  static constexpr int ACOP = 2, BCOP = 2, NCOPY = 24, ECOP = 3, NJ = 2, CSTEP = 2, TGW = 4;
+  static constexpr int STAGES = 2, STAGE = 33024, EPOCH = 4, SC_ROWS = 384, STG = 4096, BLOCKS_PER_CU = 2;
 };
-constexpr int PF_STG = 6144;                         // per-wave output staging after the K loop
+template <bool W> constexpr int pf_lds_bytes() {
+  using Sh = PfShape<W>;
+  static_assert(Sh::B_OFF + Sh::N * 64 <= Sh::STAGE && 2 * Sh::R + Sh::N <= Sh::SC_ROWS, "stage layout");
+  static_assert(Sh::SC_ROWS * 4 * Sh::EPOCH == 256 * Sh::NCOPY && 8 * Sh::ECOP >= Sh::NCOPY, "epoch copies");
+  static_assert(8 * Sh::STG <= Sh::STAGES * Sh::STAGE, "output staging inside the ring");
+  return Sh::STAGES * Sh::STAGE + 2 * Sh::SC_ROWS * 4 * Sh::EPOCH;
+}
+static_assert(PfShape<true>::BLOCKS_PER_CU * (pf_lds_bytes<true>() + 4 * PfShape<true>::R) <= 163840 &&
+              PfShape<false>::BLOCKS_PER_CU * (pf_lds_bytes<false>() + 4 * PfShape<false>::R) <= 163840,
+              "workgroups per CU within 160 KB of LDS");
 constexpr int PF_GROUP = 4;                          // wide tiles whose blocks of one output block run together
 
-// s_waitcnt vmcnt(n) for the counts of the K loop (0, 5, 5 + 7, 5 + 9); a smaller count only waits longer
+// s_waitcnt vmcnt(n), n in [0, 15] (wave-uniform); a larger n waits for everything
 __device__ __forceinline__ void pf_wait(int n) {
-  if (n >= 14) __builtin_amdgcn_s_waitcnt(0x0F7E);
-  else if (n >= 12) __builtin_amdgcn_s_waitcnt(0x0F7C);
-  else if (n >= 5) __builtin_amdgcn_s_waitcnt(0x0F75);
-  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  switch (n) {
+#define PF_W(c) case c: __builtin_amdgcn_s_waitcnt(0x0F70 | c); break;
+    PF_W(1) PF_W(2) PF_W(3) PF_W(4) PF_W(5) PF_W(6) PF_W(7) PF_W(8) PF_W(9) PF_W(10) PF_W(11) PF_W(12) PF_W(13)
+    PF_W(14) PF_W(15)
+#undef PF_W
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
 }
-// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N).  Row q keeps its eight K-step words at positions
+// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N).  Row q keeps its EPOCH K-step words at positions
 // k ^ swz(q), so the scale reads of one MFMA (16 rows) fall in distinct banks.
-template <int R> __device__ __forceinline__ int pf_swz(int q) {
-  return ((q >> 2) ^ ((q >= R && q < 2 * R) ? 2 : 0)) & 3;
+template <int EP, int R> __device__ __forceinline__ int pf_swz(int q) {
+  if constexpr (EP == 8) return ((q >> 2) ^ ((q >= R && q < 2 * R) ? 2 : 0)) & 3;   // 32-byte rows
+  else return (q >> 3) & 3;                                                        // 16-byte rows
 }
 #define PF_MFMA(A, B, C, SA, SB) __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 0, 4, 0, (SA), 0, (SB))
 
@@ -95,7 +112,9 @@ template <bool GATEUP, bool WIDE>
 __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* s_tok, int slot, int beg, int nvalid,
                                         int ob) {
   using Sh = PfShape<WIDE>;
-  constexpr int R = Sh::R, N = Sh::N, NJ = Sh::NJ;
+  constexpr int R = Sh::R, N = Sh::N, NJ = Sh::NJ, EP = Sh::EPOCH;
+  constexpr int PF_SC = Sh::STAGES * Sh::STAGE;
+  constexpr int SCB = Sh::SC_ROWS * 4 * EP;      // bytes of one epoch buffer
   constexpr int HALF = GATEUP ? N / 2 : N;       // block rows of one projection
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -137,39 +156,42 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   const int brow_c = (N / 8) * wave;
   const uint32_t b_off = (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 2)) * (uint32_t)(K / 2) +
                          16u * (uint32_t)(((lane & 3) - (lane >> 4)) & 3);
-  // scale copies: copy c covers epoch rows 8 (ECOP wave + c) .. + 7, eight lanes per row
+  // scale copies: copy c covers epoch rows (64 / EP) (ECOP wave + c) .., EP lanes (words) per row
   const uint8_t* bs_base = (GATEUP ? a.gate_s[pool] : a.down_s[pool]) + (ps * ncol + n0) * KS;
   const uint8_t* us_base = a.up_s[pool] + (ps * ncol + n0) * KS;
   uint32_t e_off[Sh::ECOP], e_k4[Sh::ECOP];
   const uint8_t* e_src[Sh::ECOP];
 #pragma unroll
   for (int c = 0; c < Sh::ECOP; ++c) {
-    const int q0 = 8 * (Sh::ECOP * wave + c);
-    e_src[c] = q0 < R ? a_hs : q0 < 2 * R ? a_ls : (GATEUP && q0 - 2 * R >= HALF) ? us_base : bs_base;
-    // the lane's word position lane & 7 holds K-step (lane & 7) ^ swz(row) of the epoch
-    const int q = q0 + (lane >> 3);
-    e_k4[c] = 4u * (uint32_t)((lane & 7) ^ pf_swz<R>(q));
+    const int q0 = (64 / EP) * (Sh::ECOP * wave + c);
+    e_src[c] = q0 < R ? a_hs : q0 < 2 * R ? a_ls : (GATEUP && q0 - 2 * R >= HALF && q0 - 2 * R < N) ? us_base : bs_base;
+    // the lane's word position lane % EP holds K-step (lane % EP) ^ swz(row) of the epoch
+    const int q = q0 + lane / EP;
+    e_k4[c] = 4u * (uint32_t)((lane % EP) ^ pf_swz<EP, R>(q));
     if (q < 2 * R) {
       const int r = q < R ? q : q - R;
       e_off[c] = (uint32_t)s_tok[r < nvalid ? r : 0] * (uint32_t)KS;
-    } else {
+    } else if (q < 2 * R + N) {
       const int br = q - 2 * R;
       e_off[c] = (uint32_t)(br - ((GATEUP && br >= HALF) ? HALF : 0)) * (uint32_t)KS;
+    } else {
+      e_off[c] = 0;                              // padding rows of the buffer: never read
     }
   }
 
   auto issue_epoch = [&](int e) __attribute__((always_inline)) {
-    uint8_t* dst = pl + PF_SC + (e & 1) * PF_SC_BYTES;
+    uint8_t* dst = pl + PF_SC + (e & 1) * SCB;
 #pragma unroll
     for (int c = 0; c < Sh::ECOP; ++c) {
-      // words past the row's end (K < 1024) read the row's first word instead; they are never used
-      const uint32_t kk = 32u * (uint32_t)e + e_k4[c];
-      lds_copy4(e_src[c], e_off[c] + (kk < (uint32_t)KS ? kk : 0u), dst + 256 * (Sh::ECOP * wave + c));
+      // words past the row's end read the row's first word instead; they are never used
+      const uint32_t kk = 4u * EP * (uint32_t)e + e_k4[c];
+      if (Sh::ECOP * wave + c < Sh::NCOPY)
+        lds_copy4(e_src[c], e_off[c] + (kk < (uint32_t)KS ? kk : 0u), dst + 256 * (Sh::ECOP * wave + c));
     }
   };
   auto issue = [&](int s) __attribute__((always_inline)) {   // K-step s into ring slot s % 3 (and its epoch's scales)
-    if (s % PF_EPOCH == 0) issue_epoch(s / PF_EPOCH);
-    uint8_t* st = pl + (s % PF_STAGES) * PF_STAGE;
+    if (s % EP == 0) issue_epoch(s / EP);
+    uint8_t* st = pl + (s % Sh::STAGES) * Sh::STAGE;
     const uint32_t k0 = (uint32_t)s * 128u;
 #pragma unroll
     for (int c = 0; c < Sh::ACOP; ++c) lds_copy16(a_src[c], a_off[c] + k0, st + a_dst[c]);
@@ -181,8 +203,8 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 
   // the wave's tiles: weight rows 64 tg .. (GATEUP t = 2 p + b: projection p, 16-output half b), chunks
   // cb + CSTEP j (routes 16 chunk ..) for the live j
-  const int tg = WIDE ? (wave & 3) : wave;
-  const int cb = WIDE ? (wave >> 2) : 0;
+  const int tg = wave % Sh::TGW;
+  const int cb = wave / Sh::TGW;
   uint32_t live = 0;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) live |= (PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
@@ -191,8 +213,8 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     brow[t] = GATEUP ? (t >> 1) * HALF + 32 * tg + 16 * (t & 1) + i : 64 * tg + 16 * t + i;
-    bsc[t] = 32 * (2 * R + brow[t]) + g;
-    bsw[t] = pf_swz<R>(2 * R + brow[t]);
+    bsc[t] = 4 * EP * (2 * R + brow[t]) + g;
+    bsw[t] = pf_swz<EP, R>(2 * R + brow[t]);
   }
   const int bslot = 16 * ((g + (i >> 2)) & 3);
   // A operand of chunk j, plane p: route row r = 16 chunk + i, chunks g and 4 + g of its 128 codes
@@ -203,8 +225,8 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     aoff[j] = 128 * r;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      asc[j][p] = 32 * (p * R + r) + g;
-      asw[j][p] = pf_swz<R>(p * R + r);
+      asc[j][p] = 4 * EP * (p * R + r) + g;
+      asw[j][p] = pf_swz<EP, R>(p * R + r);
     }
   }
   const int sw_lo = 16 * (g ^ (i & 7)), sw_hi = 16 * ((4 + g) ^ (i & 7));
@@ -214,16 +236,19 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[j][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
+  constexpr int AHEAD = Sh::STAGES - 1;          // K-steps in flight while one is multiplied
+  const int n_ecop = __builtin_amdgcn_readfirstlane(max(0, min(Sh::ECOP, Sh::NCOPY - Sh::ECOP * wave)));
   issue(0);
-  if (nK > 1) issue(1);
+  if (AHEAD == 2 && nK > 1) issue(1);
   for (int s = 0; s < nK; ++s) {
-    // copies issued after step s's: step s + 1's five, plus its epoch's scales when it opens one
-    pf_wait(s + 1 < nK ? 5 + (((s + 1) % PF_EPOCH == 0) ? Sh::ECOP : 0) : 0);
+    // copies issued after step s's: AHEAD 2: step s + 1's, with its epoch's scales when it opens one; AHEAD 1: none
+    if constexpr (AHEAD == 2) pf_wait(s + 1 < nK ? Sh::ACOP + Sh::BCOP + ((s + 1) % EP == 0 ? n_ecop : 0) : 0);
+    else pf_wait(0);
     __syncthreads();                             // step s landed everywhere; step s - 1's slot is free
-    if (s + 2 < nK) issue(s + 2);
-    const uint8_t* st = pl + (s % PF_STAGES) * PF_STAGE;
-    const uint8_t* sc = pl + PF_SC + ((s / PF_EPOCH) & 1) * PF_SC_BYTES;
-    const int kw = s % PF_EPOCH;
+    if (s + AHEAD < nK) issue(s + AHEAD);
+    const uint8_t* st = pl + (s % Sh::STAGES) * Sh::STAGE;
+    const uint8_t* sc = pl + PF_SC + ((s / EP) & 1) * SCB;
+    const int kw = s % EP;
     v8i B[4];
     int sb[4];
 #pragma unroll
@@ -260,7 +285,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   // stores are 16 bytes per lane.
   mfma_f8f4_settle();
   __syncthreads();
-  uint8_t* stg = pl + PF_STG * wave;
+  uint8_t* stg = pl + Sh::STG * wave;
   if constexpr (GATEUP) {
     // staging: [16 NJ routes][hi 32 bytes | lo 32 bytes], then the routes' (hi, lo) scale bytes
     uint8_t* ssc = stg + 64 * PF_UNIT * NJ;
@@ -349,43 +374,37 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   }
 }
 
-// One launch covers both tile shapes.  Workgroups go to the 8 XCDs round robin (hardware block b runs on XCD
-// b % 8); XCD x takes the x-th eighth of the wide (tile, output block) list and of the narrow one (output blocks
-// fastest), interleaved in proportion so MFMA-bound wide blocks and HBM-bound narrow blocks run side by side.
-// The 1-D grid has at least 8 ceil(used / 8) blocks per list; the rest exit at once.
-template <bool GATEUP>
-__global__ void __launch_bounds__(512) prefill_gemm_kernel(PrefillArgs a) {
+// One launch per tile shape (the narrow tiles first, then the wide ones).  Workgroups go to the 8 XCDs round
+// robin (hardware block b runs on XCD b % 8); XCD x takes the x-th eighth of the shape's (tile, output block)
+// list.  The 1-D grid has 8 ceil(bound / 8) blocks; those past the used pairs exit at once.
+template <bool GATEUP, bool WIDE>
+__global__ void __launch_bounds__(512, PfShape<WIDE>::BLOCKS_PER_CU) prefill_gemm_kernel(PrefillArgs a) {
+  using Sh = PfShape<WIDE>;
   extern __shared__ __align__(256) uint8_t pl[];
-  __shared__ int s_tok[PF_WIDE_ROWS];
+  __shared__ int s_tok[Sh::R];
   const int4 hdr = a.tiles[0];                   // (wide tiles, narrow tiles)
-  const int obW = GATEUP ? a.I / 128 : a.H / 256;
-  const int obS = GATEUP ? a.I / 256 : a.H / 512;
-  const int usedW = __builtin_amdgcn_readfirstlane(hdr.x) * obW;
-  const int usedS = __builtin_amdgcn_readfirstlane(hdr.y) * obS;
-  const int perW = (usedW + 7) / 8, perS = (usedS + 7) / 8;
+  const int nt = __builtin_amdgcn_readfirstlane(WIDE ? hdr.x : hdr.y);
+  const int obn = GATEUP ? a.I / (Sh::N / 2) : a.H / Sh::N;   // output blocks per tile
+  const int used = nt * obn, per = (used + 7) / 8;
   const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
-  const int nWx = max(0, min(perW, usedW - x * perW)), nSx = max(0, min(perS, usedS - x * perS));
-  const int n = nWx + nSx;
-  if (j >= n) return;
-  const int wb = (int)(((long long)j * nWx) / n);           // wide blocks before position j
-  if ((int)(((long long)(j + 1) * nWx) / n) > wb) {
-    // wide list order: groups of PF_GROUP consecutive tiles (a popular slot's tiles are consecutive), output block,
-    // then tile, so the blocks that run together on an XCD share each weight block between PF_GROUP tiles and each
-    // tile's activations between the group's output blocks; the last group may hold fewer tiles
-    const int l = x * perW + wb;
-    const int nW = __builtin_amdgcn_readfirstlane(hdr.x);
-    const int grp = l / (PF_GROUP * obW), rem = l - grp * PF_GROUP * obW;
-    const int ng = min(PF_GROUP, nW - grp * PF_GROUP);
-    const int ob = rem / ng, tile = grp * PF_GROUP + (rem - ob * ng);
-    const int4 tt = a.tiles[1 + tile];
-    pf_tile<GATEUP, true>(a, pl, s_tok, __builtin_amdgcn_readfirstlane(tt.x), __builtin_amdgcn_readfirstlane(tt.y),
-                          __builtin_amdgcn_readfirstlane(tt.z - tt.y), ob);
+  if (j >= max(0, min(per, used - x * per))) return;
+  const int l = x * per + j;
+  int tile, ob;
+  if constexpr (WIDE) {
+    // groups of PF_GROUP consecutive tiles (a popular slot's tiles are consecutive), output block, then tile, so
+    // the blocks that run together on an XCD share each weight block between PF_GROUP tiles and each tile's
+    // activations between the group's output blocks; the last group may hold fewer tiles
+    const int grp = l / (PF_GROUP * obn), rem = l - grp * PF_GROUP * obn;
+    const int ng = min(PF_GROUP, nt - grp * PF_GROUP);
+    ob = rem / ng;
+    tile = grp * PF_GROUP + (rem - ob * ng);
   } else {
-    const int l = x * perS + (j - wb), tile = l / obS;
-    const int4 tt = a.tiles[1 + a.wcap + tile];
-    pf_tile<GATEUP, false>(a, pl, s_tok, __builtin_amdgcn_readfirstlane(tt.x), __builtin_amdgcn_readfirstlane(tt.y),
-                           __builtin_amdgcn_readfirstlane(tt.z - tt.y), l - tile * obS);
+    tile = l / obn;                              // output blocks fastest
+    ob = l - tile * obn;
   }
+  const int4 tt = a.tiles[1 + (WIDE ? 0 : a.wcap) + tile];
+  pf_tile<GATEUP, WIDE>(a, pl, s_tok, __builtin_amdgcn_readfirstlane(tt.x), __builtin_amdgcn_readfirstlane(tt.y),
+                        __builtin_amdgcn_readfirstlane(tt.z - tt.y), ob);
 }
 
 // ------------------------------------------------------------------ weighted combine in route order
@@ -438,7 +457,7 @@ struct PrefillWs {
 };
 
 // Tile capacities: a wide tile holds more than narrow_max routes (or, with narrow tiles off, at least one), so
-// sum_s ceil(count_s / 96) <= P / 96 + #{s : count_s > narrow_max}; at most one narrow tile per slot.
+// sum_s ceil(count_s / 64) <= P / 64 + #{s : count_s > narrow_max}; at most one narrow tile per slot.
 struct PfTiling {
   int narrow_max, wcap, scap;
 };
@@ -482,6 +501,45 @@ static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int 
 __global__ void reset_status_kernel(int32_t* status) { status[0] = 0; }
 
 // stage (optional): a second bank whose slots follow the bank's (slot ids bank->n_slots ...)
+// The narrow tiles of a GEMM run on a side stream of the device (default priority, created with two events on
+// the device's first prefill call) concurrently with the wide tiles on the caller's stream: the narrow launch
+// waits for the work queued on the caller's stream, and the caller's stream waits for the narrow launch before
+// its next work.  The fork and join of one call are enqueued under a lock, so calls from several host threads
+// never wait on each other's events; their narrow launches queue one after another on the side stream.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex mu;
+};
+static SideStream* side_stream() {
+  static std::mutex mu;
+  static SideStream per[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> g(mu);
+  SideStream& ss = per[dev];
+  if (!ss.s) {
+    if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) {
+      (void)hipStreamDestroy(ss.s);
+      ss.s = nullptr;
+      return nullptr;
+    }
+  }
+  return &ss;
+}
+
+template <bool GATEUP, bool WIDE> static int pf_allow_lds() {
+  static int allowed = 0;
+  if (allowed) return MIMO_OK;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<GATEUP, WIDE>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, pf_lds_bytes<WIDE>());
+  if (e != hipSuccess) return set_error(MIMO_ERR_HIP, "prefill LDS attribute: %s", hipGetErrorString(e));
+  allowed = 1;
+  return MIMO_OK;
+}
+
 static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* wts, int k, const mimo_bank* bank,
                        const mimo_bank* stage, uint16_t* y, const PrefillWs& ws, hipStream_t st,
                        const uint16_t* resid = nullptr) {
@@ -512,28 +570,44 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   a.sigtab = sig;
   a.hq_hi = ws.hq_hi; a.hq_lo = ws.hq_lo; a.hq_hs = ws.hq_hs; a.hq_ls = ws.hq_ls;
   a.Y = ws.Y; a.y = y;
-  static int allowed_gu = 0, allowed_dn = 0;
-  if (!allowed_gu) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
-    if (e != hipSuccess) return set_error(MIMO_ERR_HIP, "prefill LDS attribute: %s", hipGetErrorString(e));
-    allowed_gu = 1;
-  }
-  if (!allowed_dn) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<false>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
-    if (e != hipSuccess) return set_error(MIMO_ERR_HIP, "prefill LDS attribute: %s", hipGetErrorString(e));
-    allowed_dn = 1;
-  }
-  // 1-D grids: 8 x (ceil(wide bound / 8) + ceil(narrow bound / 8)) blocks, so every XCD has an index for each
-  // of its (tile, output block) pairs; blocks past the used pairs exit at once
-  auto grid_of = [&](int obW, int obS) {
-    return 8 * (int)(((int64_t)tl.wcap * obW + 7) / 8 + ((int64_t)tl.scap * obS + 7) / 8);
+  int rc2 = pf_allow_lds<true, true>();
+  if (!rc2) rc2 = pf_allow_lds<true, false>();
+  if (!rc2) rc2 = pf_allow_lds<false, true>();
+  if (!rc2) rc2 = pf_allow_lds<false, false>();
+  if (rc2) return rc2;
+  // 1-D grids of 8 ceil(bound / 8) blocks per shape, so every XCD has an index for each of its (tile, output
+  // block) pairs; blocks past the used pairs exit at once.  The narrow (HBM-bound) tiles run first, then the wide
+  // tiles with two workgroups per CU.
+  auto grid_of = [&](int cap, int obn) { return 8 * (int)(((int64_t)cap * obn + 7) / 8); };
+  using NS = PfShape<false>;
+  using WS = PfShape<true>;
+  SideStream* ss = tl.scap ? side_stream() : nullptr;
+  if (tl.scap && !ss) return set_error(MIMO_ERR_HIP, "moe prefill: cannot create the side stream");
+  // one GEMM: narrow tiles on the side stream, wide tiles on st, joined before st's next work
+  auto gemm = [&](auto narrow_kernel, auto wide_kernel, int obn_narrow, int obn_wide) -> int {
+    if (!ss) {
+      wide_kernel<<<grid_of(tl.wcap, obn_wide), 512, pf_lds_bytes<true>(), st>>>(a);
+      return MIMO_OK;
+    }
+    std::lock_guard<std::mutex> g(ss->mu);
+    MIMO_HIP(hipEventRecord(ss->fork, st));
+    MIMO_HIP(hipStreamWaitEvent(ss->s, ss->fork, 0));
+    narrow_kernel<<<grid_of(tl.scap, obn_narrow), 512, pf_lds_bytes<false>(), ss->s>>>(a);
+    wide_kernel<<<grid_of(tl.wcap, obn_wide), 512, pf_lds_bytes<true>(), st>>>(a);
+    MIMO_HIP(hipEventRecord(ss->join, ss->s));
+    MIMO_HIP(hipStreamWaitEvent(st, ss->join, 0));
+    return MIMO_OK;
   };
-  const int grid_gu = grid_of(I / 128, I / 256);
-  const int grid_dn = grid_of(H / 256, H / 512);
-  { ProfScope p(st, "prefill_gateup"); prefill_gemm_kernel<true><<<grid_gu, 512, PF_LDS, st>>>(a); }
-  { ProfScope p(st, "prefill_down"); prefill_gemm_kernel<false><<<grid_dn, 512, PF_LDS, st>>>(a); }
+  {
+    ProfScope p(st, "prefill_gateup");
+    int rc3 = gemm(prefill_gemm_kernel<true, false>, prefill_gemm_kernel<true, true>, I / (NS::N / 2), I / (WS::N / 2));
+    if (rc3) return rc3;
+  }
+  {
+    ProfScope p(st, "prefill_down");
+    int rc3 = gemm(prefill_gemm_kernel<false, false>, prefill_gemm_kernel<false, true>, H / NS::N, H / WS::N);
+    if (rc3) return rc3;
+  }
   { ProfScope p(st, "prefill_combine");
     prefill_combine_kernel<<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, resid, y); }
   return check_launch("moe prefill");
