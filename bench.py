@@ -542,7 +542,7 @@ def traffic_parse(fetch_dir, write_dir):
         out[f"_detail_{tag}"] = {"kernel": pname, "dispatches": len(pf_), "fetch_bytes": pfetch,
                                  "write_bytes": pwrite, "algorithmic_bytes": algo_pf[gate],
                                  "distinct_experts": U}
-        rows.append((f"prefill_gemm_kernel<{'true' if gate else 'false'}> ({T} tokens, {U:.1f} experts)",
+        rows.append((f"prefill {'gate/up' if gate else 'down'} GEMM, narrow + wide launches ({T} tokens, {U:.1f} experts)",
                      len(pf_), pfetch, pwrite, algo_pf[gate]))
     with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as fh:
         json.dump(out, fh, indent=1)
