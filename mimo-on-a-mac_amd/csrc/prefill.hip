@@ -58,8 +58,8 @@ constexpr int PF_WIDE_ROWS = 64;
 constexpr int PF_UNIT = 16;                          // routes per MFMA chunk
 
 // Stage layout: A planes of R routes x 128 codes, the 16-byte chunk q of route r at slot q ^ (r & 7), the lo
-// plane 128 bytes off the hi plane's bank phase; B rows of 64 bytes, chunk g of row r at slot (g + (r & 15) / 4)
-// & 3.  Both make the MFMA operand reads conflict-free.  Copies per wave: ACOP + BCOP per K-step (one per
+// plane 128 bytes off the hi plane's bank phase; B rows of 64 bytes, chunk g of row r at slot (g + (r & 15) / 2)
+// & 3.  Both make the MFMA operand reads conflict-free (gfx950 LDS, measured with the bank-conflict counter).  Copies per wave: ACOP + BCOP per K-step (one per
 // 8-route block of a plane or 16 weight rows), up to ECOP of the NCOPY epoch copies per epoch.  A wave
 // multiplies 4 weight tiles (64 rows) by NJ 16-route chunks spaced CSTEP apart; TGW waves cover the N rows.
 // The ring holds STAGES steps of STAGE bytes, then two epoch buffers of SC_ROWS rows (2R + N used); STG bytes
@@ -147,7 +147,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     a_src[c] = b >= Sh::CB ? a_lo : a_hi;
     a_dst[c] = (b >= Sh::CB ? Sh::A_PL : 0) + 1024 * (b % Sh::CB);
   }
-  // B copies: block rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding chunk (slot - row / 4) & 3
+  // B copies: block rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding chunk (slot - row / 2) & 3
   const bool up_half = GATEUP && wave >= 4;
   const int pool = slot >= a.S0;                 // tile-uniform: the bank or the staging bank
   const size_t ps = (size_t)(slot - (pool ? a.S0 : 0));
@@ -155,7 +155,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   const uint8_t* bw_base = reinterpret_cast<const uint8_t*>(bw) + (ps * ncol + n0) * (K / 2);
   const int brow_c = (N / 8) * wave;
   const uint32_t b_off = (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 2)) * (uint32_t)(K / 2) +
-                         16u * (uint32_t)(((lane & 3) - (lane >> 4)) & 3);
+                         16u * (uint32_t)(((lane & 3) - (lane >> 3)) & 3);
   // scale copies: copy c covers epoch rows (64 / EP) (ECOP wave + c) .., EP lanes (words) per row
   const uint8_t* bs_base = (GATEUP ? a.gate_s[pool] : a.down_s[pool]) + (ps * ncol + n0) * KS;
   const uint8_t* us_base = a.up_s[pool] + (ps * ncol + n0) * KS;
@@ -216,7 +216,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     bsc[t] = 4 * EP * (2 * R + brow[t]) + g;
     bsw[t] = pf_swz<EP, R>(2 * R + brow[t]);
   }
-  const int bslot = 16 * ((g + (i >> 2)) & 3);
+  const int bslot = 16 * ((g + (i >> 1)) & 3);
   // A operand of chunk j, plane p: route row r = 16 chunk + i, chunks g and 4 + g of its 128 codes
   int aoff[NJ], asc[NJ][2], asw[NJ][2];
 #pragma unroll

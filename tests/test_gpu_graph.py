@@ -43,3 +43,44 @@ def test_prefill_and_decode_graph_replays_match_eager(rng):
         blk(other)                                   # eager work on the same workspaces between replays
         blk._moe_prefill(other, inds, w)
         torch.cuda.synchronize()
+
+
+def test_prefill_from_two_host_threads_on_two_streams(rng):
+    """Two host threads run prefills of different inputs on two streams of the same device at once: the narrow
+    tiles of both share the library's side stream, and each call's fork and join must wait on its own stream's
+    work only, so both results equal the single-threaded ones."""
+    import threading
+    from mimo_stream import pools, Router, MoEBlock
+    H, I, E, k = 4096, 2048, 64, 8
+    bank = pools.random_bank(E, seed=78, hidden=H, inter=I)
+    r = Router(H, E, k)
+    r.weight.copy_(to_dev_bf16(rand_bf16(rng, (E, H), 0.02)))
+    blocks = [MoEBlock(r, bank), MoEBlock(r, bank)]       # separate status words; same weights
+    T = 300
+    xs = [to_dev_bf16(rand_bf16(rng, (T, H))) for _ in range(2)]
+    routes = [torch.from_numpy(zipf_routes(rng, T, E, k)).cuda() for _ in range(2)]
+    ws = [torch.from_numpy(rng.random((T, k)).astype(np.float32)).cuda() for _ in range(2)]
+    want = [blocks[i]._moe_prefill(xs[i], routes[i], ws[i]) for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    got = [[None] * 4, [None] * 4]
+    errors = []
+
+    def run(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                for rep in range(4):
+                    got[i][rep] = blocks[i]._moe_prefill(xs[i], routes[i], ws[i])
+            streams[i].synchronize()
+        except Exception as e:          # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for rep in range(4):
+            assert torch.equal(got[i][rep], want[i]), (i, rep)
