@@ -408,41 +408,57 @@ __global__ void __launch_bounds__(512, PfShape<WIDE>::BLOCKS_PER_CU) prefill_gem
 }
 
 // ------------------------------------------------------------------ weighted combine in route order
-// y[t] = bf16(sum_j fp32(Y[inv[t*k + j]]) * w[t, j]), j ascending (model.py:269-271).
+// y[t] = bf16(sum_j fp32(Y[inv[t*k + j]]) * w[t, j]), j ascending (model.py:269-271).  A thread owns 8 outputs
+// (16-byte loads); all k route rows are requested before the sum.
 __global__ void __launch_bounds__(256) prefill_combine_kernel(const uint16_t* __restrict__ Y, const int32_t* __restrict__ inv,
                                                               const float* __restrict__ w, int k, int H,
                                                               const uint16_t* resid, uint16_t* y) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
-  const int m = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int m = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (m >= H) return;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int j = 0; j < k; ++j) {
-    const int p = inv[t * k + j];
-    const float wj = w[t * k + j];
-    const uint2 v = *reinterpret_cast<const uint2*>(Y + (size_t)p * H + m);
-    float f[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y << 16),
-                  __uint_as_float(v.y & 0xFFFF0000u)};
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int KB = 8;                          // routes whose rows are in flight at once
+  for (int j0 = 0; j0 < k; j0 += KB) {
+    uint4 v[KB];
+    float wj[KB];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float prod = f[q] * wj;
-      acc[q] = acc[q] + prod;
+    for (int jj = 0; jj < KB; ++jj) {
+      const int j = j0 + jj < k ? j0 + jj : j0;
+      v[jj] = *reinterpret_cast<const uint4*>(Y + (size_t)inv[t * k + j] * H + m);
+      wj[jj] = w[t * k + j];
+    }
+#pragma unroll
+    for (int jj = 0; jj < KB; ++jj) {
+      if (j0 + jj >= k) break;
+      const uint32_t u[4] = {v[jj].x, v[jj].y, v[jj].z, v[jj].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = __uint_as_float(u[q] << 16), hi = __uint_as_float(u[q] & 0xFFFF0000u);
+        const float plo = lo * wj[jj], phi = hi * wj[jj];
+        acc[2 * q] = acc[2 * q] + plo;
+        acc[2 * q + 1] = acc[2 * q + 1] + phi;
+      }
     }
   }
-  uint16_t yb[4];
+  uint16_t yb[8];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) yb[q] = f32_to_bf16(acc[q]);
+  for (int q = 0; q < 8; ++q) yb[q] = f32_to_bf16(acc[q]);
   if (resid) {                       // h = x + y of the decoder layer (resid may alias y: read before the write)
-    const uint2 rv = *reinterpret_cast<const uint2*>(resid + (size_t)t * H + m);
-    yb[0] = residual_bf16((uint16_t)rv.x, yb[0]);
-    yb[1] = residual_bf16((uint16_t)(rv.x >> 16), yb[1]);
-    yb[2] = residual_bf16((uint16_t)rv.y, yb[2]);
-    yb[3] = residual_bf16((uint16_t)(rv.y >> 16), yb[3]);
+    const uint4 rv = *reinterpret_cast<const uint4*>(resid + (size_t)t * H + m);
+    const uint32_t r[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      yb[2 * q] = residual_bf16((uint16_t)r[q], yb[2 * q]);
+      yb[2 * q + 1] = residual_bf16((uint16_t)(r[q] >> 16), yb[2 * q + 1]);
+    }
   }
-  uint2 o;
+  uint4 o;
   o.x = (uint32_t)yb[0] | ((uint32_t)yb[1] << 16);
   o.y = (uint32_t)yb[2] | ((uint32_t)yb[3] << 16);
-  *reinterpret_cast<uint2*>(y + (size_t)t * H + m) = o;
+  o.z = (uint32_t)yb[4] | ((uint32_t)yb[5] << 16);
+  o.w = (uint32_t)yb[6] | ((uint32_t)yb[7] << 16);
+  *reinterpret_cast<uint4*>(y + (size_t)t * H + m) = o;
 }
 
 // ------------------------------------------------------------------ host
@@ -609,7 +625,7 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
     if (rc3) return rc3;
   }
   { ProfScope p(st, "prefill_combine");
-    prefill_combine_kernel<<<dim3((H + 1023) / 1024, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, resid, y); }
+    prefill_combine_kernel<<<dim3((H + 2047) / 2048, T), 256, 0, st>>>(ws.Y, ws.inv, wts, k, H, resid, y); }
   return check_launch("moe prefill");
 }
 
