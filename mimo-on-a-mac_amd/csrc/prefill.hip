@@ -377,8 +377,10 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 // One launch per tile shape (the narrow tiles first, then the wide ones).  Workgroups go to the 8 XCDs round
 // robin (hardware block b runs on XCD b % 8); XCD x takes the x-th eighth of the shape's (tile, output block)
 // list.  The 1-D grid has 8 ceil(bound / 8) blocks; those past the used pairs exit at once.
+// (The second launch bound is the minimum number of waves per SIMD: 8 waves per block x BLOCKS_PER_CU over 4 SIMDs,
+// so the wide kernel must fit two blocks' waves in the register file: at most 128 VGPRs.)
 template <bool GATEUP, bool WIDE>
-__global__ void __launch_bounds__(512, PfShape<WIDE>::BLOCKS_PER_CU) prefill_gemm_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(512, 2 * PfShape<WIDE>::BLOCKS_PER_CU) prefill_gemm_kernel(PrefillArgs a) {
   using Sh = PfShape<WIDE>;
   extern __shared__ __align__(256) uint8_t pl[];
   __shared__ int s_tok[Sh::R];
