@@ -5,15 +5,15 @@
 // gather_qmm calls, bf16 SwiGLU intermediate, bf16 expert outputs, inverse permutation, (Y.f32 * w).sum(1)).
 //
 // Tiling: the dispatch cuts each slot's sorted routes into row tiles (narrow: a slot of at most 32 routes;
-// wide: up to 64 routes) and writes the tile table.  A block (8 waves) owns one row tile and one block of
-// weight rows (narrow 512, wide 256; gate/up blocks take half of their rows from each projection).  Each GEMM
-// is two launches that run concurrently: the narrow tiles (HBM-bound) on a side stream, one workgroup per CU
-// with a 3-slot LDS ring, and the wide tiles (MFMA work of popular experts) on the caller's stream, two
-// workgroups per CU with a 2-slot ring, so one workgroup's MFMAs run while the other waits at its barrier.
-// The K loop runs in steps of 128 through the ring, filled by global_load_lds (activation hi and lo E4M3 planes
-// of the tile's routes, the block's E2M1 weight rows; E8M0 scales once per epoch of steps); each wave
-// multiplies 16-route chunks by four 16-row weight tiles, the hi and lo planes accumulating into the same
-// tile.  The epilogue stages results in LDS and writes 16-byte pieces.
+// wide: up to 64 routes) and writes the tile table.  A block (8 waves) owns one row tile and 256 weight rows
+// (gate/up blocks take half of their rows from each projection).  Each GEMM is two launches that run
+// concurrently: the narrow tiles (HBM-bound) on a side stream, one workgroup per CU with a 3-slot LDS ring, and
+// the wide tiles (MFMA work of popular experts) on the caller's stream, two workgroups per CU with a 2-slot ring,
+// so one workgroup's MFMAs run while the other waits at its barrier.  The K loop runs through the ring in steps
+// of 256 codes (narrow) or 128 (wide), filled by global_load_lds (activation hi and lo E4M3 planes of the tile's
+// routes, the block's E2M1 weight rows; E8M0 scales once per epoch); each wave multiplies 16-route chunks by
+// four 16-row weight tiles, the hi and lo planes accumulating into the same tile.  The epilogue stages results in
+// LDS and writes 16-byte pieces.
 #include <mutex>
 
 #include "device.h"
@@ -41,43 +41,51 @@ struct PrefillArgs {
 };
 
 // Row tiles.  The dispatch cuts each slot's sorted routes into tiles of one of two shapes:
-//   narrow: a slot with at most 32 routes (2 chunks of 16) is one tile, multiplied by 512 weight rows per block
-//           (gate/up: 256 outputs of each projection; down: 512 outputs).  These blocks stream weights at the
-//           HBM rate with little MFMA work, so the wider weight tile halves their activation re-reads.  40 KB
-//           per K-step through a 3-slot ring (two steps in flight); 160 KB of LDS, one workgroup per CU.
+//   narrow: a slot with at most 32 routes (2 chunks of 16) is one tile, multiplied by 256 weight rows per block
+//           (gate/up: 128 outputs of each projection; down: 256 outputs).  These blocks stream weights at the
+//           HBM rate with little MFMA work.  Their K loop moves 256 codes per step, so each weight row is read
+//           128 contiguous bytes (one whole cache line) at a time: a copy probe streamed weight rows at 4.9 TB/s
+//           in 64-byte pieces and at 6.1 TB/s in 128-byte pieces.  49 KB per step through a 3-slot ring (two
+//           steps in flight); 156 KB of LDS, one workgroup per CU.
 //   wide:   a larger slot is split into ceil(count / 64) tiles of near-equal whole 16-route chunks (at most 4),
-//           multiplied by 256 weight rows per block (128 + 128 outputs, or 256 down outputs).  32 KB per
-//           K-step through a 2-slot ring; 77 KB of LDS, two workgroups per CU.
-// An MFMA multiplies 16 routes of one activation plane by 16 weight rows; the hi and lo planes accumulate into
-// the same tile, so each accumulator lane holds finished sums for 4 routes.
-// The E8M0 scales of an epoch of K-steps (narrow 8 steps, 32 bytes per row; wide 4 steps, 16 bytes) are copied
-// at once into one of two epoch buffers, one 4-byte word per lane, so scale traffic costs one request per row
-// per epoch.
+//           multiplied by 256 weight rows per block (128 + 128 outputs, or 256 down outputs).  128 codes (32 KB)
+//           per step through a 2-slot ring; 77 KB of LDS, two workgroups per CU.  The tiles of a popular slot
+//           share each weight block through L2.
+// An MFMA multiplies 16 routes of one activation plane by 16 weight rows over 128 codes (a sub-step); the hi
+// and lo planes accumulate into the same tile, so each accumulator lane holds finished sums for 4 routes.
+// The E8M0 scales of an epoch of 4 sub-steps (16 bytes per row) are copied at once into one of two epoch
+// buffers, one 4-byte word per lane, so scale traffic costs one request per row per epoch.
 constexpr int PF_NARROW_MAX = 32;
 constexpr int PF_WIDE_ROWS = 64;
 constexpr int PF_UNIT = 16;                          // routes per MFMA chunk
 
-// Stage layout: A planes of R routes x 128 codes, the 16-byte chunk q of route r at slot q ^ (r & 7), the lo
-// plane 128 bytes off the hi plane's bank phase; B rows of 64 bytes, chunk g of row r at slot (g + (r & 15) / 2)
-// & 3.  Both make the MFMA operand reads conflict-free (gfx950 LDS, measured with the bank-conflict counter).  Copies per wave: ACOP + BCOP per K-step (one per
-// 8-route block of a plane or 16 weight rows), up to ECOP of the NCOPY epoch copies per epoch.  A wave
+// Stage layout (KSUB sub-steps of 128 codes per step): per sub-step, A planes of R routes x 128 codes, the
+// 16-byte chunk q of route r at slot q ^ (r & 7), the lo plane 128 bytes off the hi plane's bank phase; then B
+// rows of 64 KSUB bytes: with KSUB 1, chunk g of row r at slot (g + (r & 15) / 2) & 3; with KSUB 2, chunk q of row
+// r at slot q ^ (r & 7).  These make the MFMA operand reads conflict-free (gfx950 LDS, measured with the
+// bank-conflict counter).  Copies per wave and step: KSUB ACOP for A (one per 8-route block of a plane and
+// sub-step) and BCOP for B (16 / KSUB weight rows each), up to ECOP of the NCOPY epoch copies per epoch.  A wave
 // multiplies 4 weight tiles (64 rows) by NJ 16-route chunks spaced CSTEP apart; TGW waves cover the N rows.
 // The ring holds STAGES steps of STAGE bytes, then two epoch buffers of SC_ROWS rows (2R + N used); STG bytes
 // per wave stage the outputs after the K loop.
 template <bool WIDE> struct PfShape;
 template <> struct PfShape<false> {
-  static constexpr int R = 32, CB = 4, N = 512, A_PL = 4224, B_OFF = 8448;
-  static constexpr int ACOP = 1, BCOP = 4, NCOPY = 72, ECOP = 9, NJ = 2, CSTEP = 1, TGW = 8;
-  static constexpr int STAGES = 3, STAGE = 41216, EPOCH = 8, SC_ROWS = 576, STG = 6144, BLOCKS_PER_CU = 1;
+  static constexpr int R = 32, CB = 4, N = 256, A_PL = 4224, KSUB = 2, B_OFF = 16896;
+  static constexpr int ACOP = 1, BCOP = 4, NCOPY = 20, ECOP = 3, NJ = 1, CSTEP = 1, TGW = 4;
+  static constexpr int STAGES = 3, STAGE = 49664, EPOCH = 4, SC_ROWS = 320, STG = 6144, BLOCKS_PER_CU = 1;
 };
 template <> struct PfShape<true> {
-  static constexpr int R = 64, CB = 8, N = 256, A_PL = 8320, B_OFF = 16640;
+  static constexpr int R = 64, CB = 8, N = 256, A_PL = 8320, KSUB = 1, B_OFF = 16640;
   static constexpr int ACOP = 2, BCOP = 2, NCOPY = 24, ECOP = 3, NJ = 2, CSTEP = 2, TGW = 4;
   static constexpr int STAGES = 2, STAGE = 33024, EPOCH = 4, SC_ROWS = 384, STG = 4096, BLOCKS_PER_CU = 2;
 };
 template <bool W> constexpr int pf_lds_bytes() {
   using Sh = PfShape<W>;
-  static_assert(Sh::B_OFF + Sh::N * 64 <= Sh::STAGE && 2 * Sh::R + Sh::N <= Sh::SC_ROWS, "stage layout");
+  static_assert(Sh::B_OFF == Sh::KSUB * 2 * Sh::A_PL && Sh::B_OFF + Sh::N * 64 * Sh::KSUB <= Sh::STAGE &&
+                    2 * Sh::R + Sh::N <= Sh::SC_ROWS, "stage layout");
+  static_assert(Sh::TGW * 64 == Sh::N && 8 * Sh::NJ * 16 >= Sh::TGW * Sh::R && Sh::BCOP * 128 == Sh::N * Sh::KSUB,
+                "wave roles");
+  static_assert(Sh::EPOCH % Sh::KSUB == 0 && Sh::EPOCH / Sh::KSUB >= Sh::STAGES - 1, "epoch buffers reused in time");
   static_assert(Sh::SC_ROWS * 4 * Sh::EPOCH == 256 * Sh::NCOPY && 8 * Sh::ECOP >= Sh::NCOPY, "epoch copies");
   static_assert(8 * Sh::STG <= Sh::STAGES * Sh::STAGE, "output staging inside the ring");
   return Sh::STAGES * Sh::STAGE + 2 * Sh::SC_ROWS * 4 * Sh::EPOCH;
@@ -97,11 +105,11 @@ __device__ __forceinline__ void pf_wait(int n) {
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
   }
 }
-// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N).  Row q keeps its EPOCH K-step words at positions
-// k ^ swz(q), so the scale reads of one MFMA (16 rows) fall in distinct banks.
+// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N), 16 bytes each (4 sub-step words).  Row q keeps
+// its words at positions k ^ swz(q).
 template <int EP, int R> __device__ __forceinline__ int pf_swz(int q) {
-  if constexpr (EP == 8) return ((q >> 2) ^ ((q >= R && q < 2 * R) ? 2 : 0)) & 3;   // 32-byte rows
-  else return (q >> 3) & 3;                                                        // 16-byte rows
+  static_assert(EP == 4, "16-byte epoch rows");
+  return (q >> 3) & 3;
 }
 #define PF_MFMA(A, B, C, SA, SB) __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 0, 4, 0, (SA), 0, (SB))
 
@@ -147,15 +155,20 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     a_src[c] = b >= Sh::CB ? a_lo : a_hi;
     a_dst[c] = (b >= Sh::CB ? Sh::A_PL : 0) + 1024 * (b % Sh::CB);
   }
-  // B copies: block rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding chunk (slot - row / 2) & 3
+  // B copies of 16 / KSUB rows each: KSUB 1, rows brow_c + 16 c + lane / 4, the lane's slot lane & 3 holding
+  // chunk (slot - row / 2) & 3; KSUB 2, rows brow_c + 8 c + lane / 8, slot lane & 7 holding chunk slot ^ (row & 7)
   const bool up_half = GATEUP && wave >= 4;
   const int pool = slot >= a.S0;                 // tile-uniform: the bank or the staging bank
   const size_t ps = (size_t)(slot - (pool ? a.S0 : 0));
   const uint32_t* bw = GATEUP ? (up_half ? a.up_w[pool] : a.gate_w[pool]) : a.down_w[pool];
   const uint8_t* bw_base = reinterpret_cast<const uint8_t*>(bw) + (ps * ncol + n0) * (K / 2);
   const int brow_c = (N / 8) * wave;
-  const uint32_t b_off = (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 2)) * (uint32_t)(K / 2) +
-                         16u * (uint32_t)(((lane & 3) - (lane >> 3)) & 3);
+  constexpr int BRC = 16 / Sh::KSUB;             // weight rows per B copy
+  const uint32_t b_off =
+      Sh::KSUB == 1 ? (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 2)) * (uint32_t)(K / 2) +
+                          16u * (uint32_t)(((lane & 3) - (lane >> 3)) & 3)
+                    : (uint32_t)(brow_c - (up_half ? HALF : 0) + (lane >> 3)) * (uint32_t)(K / 2) +
+                          16u * (uint32_t)((lane & 7) ^ (lane >> 3));
   // scale copies: copy c covers epoch rows (64 / EP) (ECOP wave + c) .., EP lanes (words) per row
   const uint8_t* bs_base = (GATEUP ? a.gate_s[pool] : a.down_s[pool]) + (ps * ncol + n0) * KS;
   const uint8_t* us_base = a.up_s[pool] + (ps * ncol + n0) * KS;
@@ -189,25 +202,31 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
         lds_copy4(e_src[c], e_off[c] + (kk < (uint32_t)KS ? kk : 0u), dst + 256 * (Sh::ECOP * wave + c));
     }
   };
-  auto issue = [&](int s) __attribute__((always_inline)) {   // K-step s into ring slot s % 3 (and its epoch's scales)
-    if (s % EP == 0) issue_epoch(s / EP);
+  // step s (sub-steps KSUB s ..) into ring slot s % STAGES, with the scales of the epoch it opens
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    if ((Sh::KSUB * s) % EP == 0) issue_epoch(Sh::KSUB * s / EP);
     uint8_t* st = pl + (s % Sh::STAGES) * Sh::STAGE;
-    const uint32_t k0 = (uint32_t)s * 128u;
+    const uint32_t k0 = (uint32_t)s * (128u * Sh::KSUB);
 #pragma unroll
-    for (int c = 0; c < Sh::ACOP; ++c) lds_copy16(a_src[c], a_off[c] + k0, st + a_dst[c]);
+    for (int u = 0; u < Sh::KSUB; ++u)
+#pragma unroll
+      for (int c = 0; c < Sh::ACOP; ++c)
+        lds_copy16(a_src[c], a_off[c] + k0 + 128u * u, st + 2 * Sh::A_PL * u + a_dst[c]);
 #pragma unroll
     for (int c = 0; c < Sh::BCOP; ++c)
-      lds_copy16(bw_base, b_off + (uint32_t)(16 * c) * (uint32_t)(K / 2) + k0 / 2u,
-                 st + Sh::B_OFF + 64 * (brow_c + 16 * c));
+      lds_copy16(bw_base, b_off + (uint32_t)(BRC * c) * (uint32_t)(K / 2) + k0 / 2u,
+                 st + Sh::B_OFF + 64 * Sh::KSUB * (brow_c + BRC * c));
   };
 
   // the wave's tiles: weight rows 64 tg .. (GATEUP t = 2 p + b: projection p, 16-output half b), chunks
   // cb + CSTEP j (routes 16 chunk ..) for the live j
+  // (the narrow shape has MFMA work for 4 of its 8 waves; the others only copy)
   const int tg = wave % Sh::TGW;
   const int cb = wave / Sh::TGW;
+  constexpr int MWAVES = Sh::TGW * (R / PF_UNIT) / NJ;
   uint32_t live = 0;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) live |= (PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
+  for (int j = 0; j < NJ; ++j) live |= (wave < MWAVES && PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
   live = __builtin_amdgcn_readfirstlane(live);
   int brow[4], bsc[4], bsw[4];
 #pragma unroll
@@ -216,7 +235,10 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     bsc[t] = 4 * EP * (2 * R + brow[t]) + g;
     bsw[t] = pf_swz<EP, R>(2 * R + brow[t]);
   }
-  const int bslot = 16 * ((g + (i >> 1)) & 3);
+  // B operand of sub-step u: chunk 4 u + g of the row (KSUB 2) or chunk g (KSUB 1), at its swizzled slot
+  int bslot[Sh::KSUB];
+#pragma unroll
+  for (int u = 0; u < Sh::KSUB; ++u) bslot[u] = Sh::KSUB == 1 ? 16 * ((g + (i >> 1)) & 3) : 16 * ((4 * u + g) ^ (i & 7));
   // A operand of chunk j, plane p: route row r = 16 chunk + i, chunks g and 4 + g of its 128 codes
   int aoff[NJ], asc[NJ][2], asw[NJ][2];
 #pragma unroll
@@ -236,46 +258,54 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[j][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  constexpr int AHEAD = Sh::STAGES - 1;          // K-steps in flight while one is multiplied
+  constexpr int AHEAD = Sh::STAGES - 1;          // steps in flight while one is multiplied
+  const int nS = nK / Sh::KSUB;
   const int n_ecop = __builtin_amdgcn_readfirstlane(max(0, min(Sh::ECOP, Sh::NCOPY - Sh::ECOP * wave)));
   issue(0);
-  if (AHEAD == 2 && nK > 1) issue(1);
-  for (int s = 0; s < nK; ++s) {
+  if (AHEAD == 2 && nS > 1) issue(1);
+  for (int s = 0; s < nS; ++s) {
     // copies issued after step s's: AHEAD 2: step s + 1's, with its epoch's scales when it opens one; AHEAD 1: none
-    if constexpr (AHEAD == 2) pf_wait(s + 1 < nK ? Sh::ACOP + Sh::BCOP + ((s + 1) % EP == 0 ? n_ecop : 0) : 0);
+    if constexpr (AHEAD == 2)
+      pf_wait(s + 1 < nS ? Sh::KSUB * Sh::ACOP + Sh::BCOP + ((Sh::KSUB * (s + 1)) % EP == 0 ? n_ecop : 0) : 0);
     else pf_wait(0);
     __syncthreads();                             // step s landed everywhere; step s - 1's slot is free
-    if (s + AHEAD < nK) issue(s + AHEAD);
+    if (s + AHEAD < nS) issue(s + AHEAD);
     const uint8_t* st = pl + (s % Sh::STAGES) * Sh::STAGE;
-    const uint8_t* sc = pl + PF_SC + ((s / EP) & 1) * SCB;
-    const int kw = s % EP;
-    v8i B[4];
-    int sb[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint4 v = *reinterpret_cast<const uint4*>(st + Sh::B_OFF + brow[t] * 64 + bslot);
-      B[t] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
-      sb[t] = sc[bsc[t] + 4 * (kw ^ bsw[t])];
-    }
-    v8i A[NJ][2];
-    int sa[NJ][2];
+    for (int u = 0; u < Sh::KSUB; ++u) {
+      if (!live) break;                          // wave-uniform: a wave without live chunks only copies
+      const int ss = Sh::KSUB * s + u;           // sub-step: 128 codes
+      const uint8_t* sc = pl + PF_SC + ((ss / EP) & 1) * SCB;
+      const int kw = ss % EP;
+      const uint8_t* sa_st = st + 2 * Sh::A_PL * u;
+      v8i B[4];
+      int sb[4];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)                 // read unconditionally: fixed LDS counts let each MFMA group
-#pragma unroll                                   // wait for its own operands only
-      for (int p = 0; p < 2; ++p) {
-        const uint8_t* ab = st + p * Sh::A_PL + aoff[j];
-        const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + sw_lo);
-        const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + sw_hi);
-        A[j][p] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
-        sa[j][p] = sc[asc[j][p] + 4 * (kw ^ asw[j][p])];
+      for (int t = 0; t < 4; ++t) {
+        const uint4 v = *reinterpret_cast<const uint4*>(st + Sh::B_OFF + brow[t] * (64 * Sh::KSUB) + bslot[u]);
+        B[t] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+        sb[t] = sc[bsc[t] + 4 * (kw ^ bsw[t])];
       }
+      v8i A[NJ][2];
+      int sa[NJ][2];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      if (live & (1u << j)) {
+      for (int j = 0; j < NJ; ++j)               // read unconditionally: fixed LDS counts let each MFMA group
+#pragma unroll                                   // wait for its own operands only
+        for (int p = 0; p < 2; ++p) {
+          const uint8_t* ab = sa_st + p * Sh::A_PL + aoff[j];
+          const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + sw_lo);
+          const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + sw_hi);
+          A[j][p] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
+          sa[j][p] = sc[asc[j][p] + 4 * (kw ^ asw[j][p])];
+        }
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+      for (int j = 0; j < NJ; ++j) {
+        if (live & (1u << j)) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) acc[j][t] = PF_MFMA(A[j][p], B[t], acc[j][t], sa[j][p], sb[t]);
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[j][t] = PF_MFMA(A[j][p], B[t], acc[j][t], sa[j][p], sb[t]);
+        }
       }
     }
   }
@@ -374,9 +404,9 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   }
 }
 
-// One launch per tile shape (the narrow tiles first, then the wide ones).  Workgroups go to the 8 XCDs round
-// robin (hardware block b runs on XCD b % 8); XCD x takes the x-th eighth of the shape's (tile, output block)
-// list.  The 1-D grid has 8 ceil(bound / 8) blocks; those past the used pairs exit at once.
+// One launch per tile shape.  Workgroups go to the 8 XCDs round robin (hardware block b runs on XCD b % 8); XCD x
+// takes the x-th eighth of the shape's (tile, output block) list.  The 1-D grid has 8 ceil(bound / 8) blocks;
+// those past the used pairs exit at once.
 // (The second launch bound is the minimum number of waves per SIMD: 8 waves per block x BLOCKS_PER_CU over 4 SIMDs,
 // so the wide kernel must fit two blocks' waves in the register file: at most 128 VGPRs.)
 template <bool GATEUP, bool WIDE>
@@ -481,7 +511,7 @@ struct PfTiling {
 };
 static PfTiling pf_tiling(int64_t P, int S, int H, int I) {
   PfTiling t;
-  const bool narrow = I % 256 == 0 && H % 512 == 0;    // a narrow block's 512 weight rows must divide the outputs
+  const bool narrow = I % 256 == 0;    // narrow blocks: 128 (gate/up) or 256 (down) outputs, K-steps of 256
   t.narrow_max = narrow ? PF_NARROW_MAX : 0;
   t.wcap = (int)(P / PF_WIDE_ROWS + std::min<int64_t>(S, P / (t.narrow_max + 1)) + 1);
   t.scap = narrow ? (int)std::min<int64_t>(S, P) : 0;
@@ -594,8 +624,7 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   if (!rc2) rc2 = pf_allow_lds<false, false>();
   if (rc2) return rc2;
   // 1-D grids of 8 ceil(bound / 8) blocks per shape, so every XCD has an index for each of its (tile, output
-  // block) pairs; blocks past the used pairs exit at once.  The narrow (HBM-bound) tiles run first, then the wide
-  // tiles with two workgroups per CU.
+  // block) pairs; blocks past the used pairs exit at once.
   auto grid_of = [&](int cap, int obn) { return 8 * (int)(((int64_t)cap * obn + 7) / 8); };
   using NS = PfShape<false>;
   using WS = PfShape<true>;
