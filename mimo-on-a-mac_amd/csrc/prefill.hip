@@ -105,12 +105,8 @@ __device__ __forceinline__ void pf_wait(int n) {
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
   }
 }
-// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N), 16 bytes each (4 sub-step words).  Row q keeps
-// its words at positions k ^ swz(q).
-template <int EP, int R> __device__ __forceinline__ int pf_swz(int q) {
-  static_assert(EP == 4, "16-byte epoch rows");
-  return (q >> 3) & 3;
-}
+// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N), 16 bytes each (the words of 4 sub-steps).  An
+// MFMA's scale reads (16 consecutive rows, one word each) fall in 16 distinct banks.
 #define PF_MFMA(A, B, C, SA, SB) __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 0, 4, 0, (SA), 0, (SB))
 
 // One (row tile, output block).  GATEUP: A = the routes' token activations, B = gate rows [0, N/2) and up rows
@@ -172,34 +168,32 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   // scale copies: copy c covers epoch rows (64 / EP) (ECOP wave + c) .., EP lanes (words) per row
   const uint8_t* bs_base = (GATEUP ? a.gate_s[pool] : a.down_s[pool]) + (ps * ncol + n0) * KS;
   const uint8_t* us_base = a.up_s[pool] + (ps * ncol + n0) * KS;
-  uint32_t e_off[Sh::ECOP], e_k4[Sh::ECOP];
-  const uint8_t* e_src[Sh::ECOP];
-#pragma unroll
-  for (int c = 0; c < Sh::ECOP; ++c) {
-    const int q0 = (64 / EP) * (Sh::ECOP * wave + c);
-    e_src[c] = q0 < R ? a_hs : q0 < 2 * R ? a_ls : (GATEUP && q0 - 2 * R >= HALF && q0 - 2 * R < N) ? us_base : bs_base;
-    // the lane's word position lane % EP holds K-step (lane % EP) ^ swz(row) of the epoch
-    const int q = q0 + lane / EP;
-    e_k4[c] = 4u * (uint32_t)((lane % EP) ^ pf_swz<EP, R>(q));
-    if (q < 2 * R) {
-      const int r = q < R ? q : q - R;
-      e_off[c] = (uint32_t)s_tok[r < nvalid ? r : 0] * (uint32_t)KS;
-    } else if (q < 2 * R + N) {
-      const int br = q - 2 * R;
-      e_off[c] = (uint32_t)(br - ((GATEUP && br >= HALF) ? HALF : 0)) * (uint32_t)KS;
-    } else {
-      e_off[c] = 0;                              // padding rows of the buffer: never read
-    }
-  }
-
+  // The 16 rows of a copy lie in one region (region bounds are multiples of 16).  Row offsets are computed at
+  // each epoch rather than kept: a route row's from its token in s_tok, a weight row's as a wave-uniform part
+  // plus the lane's row.
+  static_assert(EP == 4 && R % 16 == 0 && HALF % 16 == 0, "16-byte epoch rows, 16-row copies");
+  const uint32_t e_k4 = 4u * (uint32_t)(lane % EP);   // the lane's word: sub-step lane % EP of the epoch
   auto issue_epoch = [&](int e) __attribute__((always_inline)) {
     uint8_t* dst = pl + PF_SC + (e & 1) * SCB;
+    // words past the row's end read the row's first word instead; they are never used
+    const uint32_t kk = 4u * EP * (uint32_t)e + e_k4;
+    const uint32_t word = kk < (uint32_t)KS ? kk : 0u;
 #pragma unroll
     for (int c = 0; c < Sh::ECOP; ++c) {
-      // words past the row's end read the row's first word instead; they are never used
-      const uint32_t kk = 4u * EP * (uint32_t)e + e_k4[c];
-      if (Sh::ECOP * wave + c < Sh::NCOPY)
-        lds_copy4(e_src[c], e_off[c] + (kk < (uint32_t)KS ? kk : 0u), dst + 256 * (Sh::ECOP * wave + c));
+      const int cc = Sh::ECOP * wave + c;        // wave-uniform
+      if (cc >= Sh::NCOPY) continue;
+      const int q0 = (64 / EP) * cc;
+      if (q0 < 2 * R) {
+        const int r = (q0 < R ? q0 : q0 - R) + lane / EP;
+        lds_copy4(q0 < R ? a_hs : a_ls, (uint32_t)s_tok[r < nvalid ? r : 0] * (uint32_t)KS + word, dst + 256 * cc);
+      } else if (q0 < 2 * R + N) {
+        const int br0 = q0 - 2 * R;
+        const bool up = GATEUP && br0 >= HALF;
+        lds_copy4(up ? us_base : bs_base, (uint32_t)(br0 - (up ? HALF : 0) + lane / EP) * (uint32_t)KS + word,
+                  dst + 256 * cc);
+      } else {
+        lds_copy4(bs_base, word, dst + 256 * cc);   // padding rows of the buffer: never read
+      }
     }
   };
   // step s (sub-steps KSUB s ..) into ring slot s % STAGES, with the scales of the epoch it opens
@@ -228,19 +222,16 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 #pragma unroll
   for (int j = 0; j < NJ; ++j) live |= (wave < MWAVES && PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
   live = __builtin_amdgcn_readfirstlane(live);
-  int brow[4], bsc[4], bsw[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    brow[t] = GATEUP ? (t >> 1) * HALF + 32 * tg + 16 * (t & 1) + i : 64 * tg + 16 * t + i;
-    bsc[t] = 4 * EP * (2 * R + brow[t]) + g;
-    bsw[t] = pf_swz<EP, R>(2 * R + brow[t]);
-  }
+  // row of tile t = brow0 + bdt(t), bdt a compile-time constant, so the tiles' LDS addresses share one register
+  auto bdt = [](int t) constexpr { return GATEUP ? (t >> 1) * HALF + 16 * (t & 1) : 16 * t; };
+  const int brow0 = (GATEUP ? 32 : 64) * tg + i;
+  const int bsc0 = 4 * EP * (2 * R + brow0) + g;
   // B operand of sub-step u: chunk 4 u + g of the row (KSUB 2) or chunk g (KSUB 1), at its swizzled slot
   int bslot[Sh::KSUB];
 #pragma unroll
   for (int u = 0; u < Sh::KSUB; ++u) bslot[u] = Sh::KSUB == 1 ? 16 * ((g + (i >> 1)) & 3) : 16 * ((4 * u + g) ^ (i & 7));
   // A operand of chunk j, plane p: route row r = 16 chunk + i, chunks g and 4 + g of its 128 codes
-  int aoff[NJ], asc[NJ][2], asw[NJ][2];
+  int aoff[NJ], asc[NJ][2];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int r = PF_UNIT * (cb + Sh::CSTEP * j) + i;
@@ -248,7 +239,6 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       asc[j][p] = 4 * EP * (p * R + r) + g;
-      asw[j][p] = pf_swz<EP, R>(p * R + r);
     }
   }
   const int sw_lo = 16 * (g ^ (i & 7)), sw_hi = 16 * ((4 + g) ^ (i & 7));
@@ -282,9 +272,10 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
       int sb[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint4 v = *reinterpret_cast<const uint4*>(st + Sh::B_OFF + brow[t] * (64 * Sh::KSUB) + bslot[u]);
+        const uint4 v = *reinterpret_cast<const uint4*>(st + Sh::B_OFF + brow0 * (64 * Sh::KSUB) + bslot[u] +
+                                                        bdt(t) * (64 * Sh::KSUB));
         B[t] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
-        sb[t] = sc[bsc[t] + 4 * (kw ^ bsw[t])];
+        sb[t] = sc[bsc0 + 4 * kw + 4 * EP * bdt(t)];
       }
       v8i A[NJ][2];
       int sa[NJ][2];
@@ -296,7 +287,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
           const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + sw_lo);
           const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + sw_hi);
           A[j][p] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
-          sa[j][p] = sc[asc[j][p] + 4 * (kw ^ asw[j][p])];
+          sa[j][p] = sc[asc[j][p] + 4 * kw];
         }
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
