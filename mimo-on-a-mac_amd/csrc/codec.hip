@@ -213,8 +213,9 @@ __global__ void dequantize_mxfp4_kernel(const uint32_t* __restrict__ q, const ui
 // ------------------------------------------------------------------ activation hi/lo split
 __global__ void quantize_fp8_hilo_kernel(const uint16_t* __restrict__ x, int64_t nblocks, uint8_t* __restrict__ hi,
                                          uint8_t* __restrict__ hs, uint8_t* __restrict__ lo,
-                                         uint8_t* __restrict__ ls) {
+                                         uint8_t* __restrict__ ls, int32_t* zero_status) {
   int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (zero_status && b == 0) *zero_status = 0;
   if (b >= nblocks) return;
   const uint4* src = reinterpret_cast<const uint4*>(x + b * 32);
   float v[32];
@@ -242,11 +243,11 @@ __global__ void quantize_fp8_hilo_kernel(const uint16_t* __restrict__ x, int64_t
 }
 
 int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint8_t* hi, uint8_t* hs, uint8_t* lo,
-                             uint8_t* ls, hipStream_t st) {
+                             uint8_t* ls, hipStream_t st, int32_t* zero_status) {
   int64_t nb = rows * (cols / 32);
   if (nb == 0) return MIMO_OK;
   ProfScope p(st, "quantize_fp8_hilo");
-  quantize_fp8_hilo_kernel<<<(int)((nb + 255) / 256), 256, 0, st>>>(x, nb, hi, hs, lo, ls);
+  quantize_fp8_hilo_kernel<<<(int)((nb + 255) / 256), 256, 0, st>>>(x, nb, hi, hs, lo, ls, zero_status);
   return check_launch("quantize_fp8_hilo");
 }
 

@@ -537,8 +537,6 @@ static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int 
   return w;
 }
 
-__global__ void reset_status_kernel(int32_t* status) { status[0] = 0; }
-
 // stage (optional): a second bank whose slots follow the bank's (slot ids bank->n_slots ...)
 // The narrow tiles of a GEMM run on a side stream of the device (default priority, created with two events on
 // the device's first prefill call) concurrently with the wide tiles on the caller's stream: the narrow launch
@@ -579,8 +577,10 @@ template <bool GATEUP, bool WIDE> static int pf_allow_lds() {
   return MIMO_OK;
 }
 
+// zero_status: the status word has not been cleared yet in this call (the activation split, queued first,
+// clears it before the dispatch may flag bad slots)
 static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const float* wts, int k, const mimo_bank* bank,
-                       const mimo_bank* stage, uint16_t* y, const PrefillWs& ws, hipStream_t st,
+                       const mimo_bank* stage, uint16_t* y, const PrefillWs& ws, hipStream_t st, bool zero_status,
                        const uint16_t* resid = nullptr) {
   const int H = bank->hidden, I = bank->inter, S = bank->n_slots + (stage ? stage->n_slots : 0);
   const int P = T * k;
@@ -592,9 +592,10 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   if (!sig) return err;
   const PfTiling tl = pf_tiling(P, S, H, I);
   const TileSpec spec{tl.narrow_max, PF_WIDE_ROWS, tl.wcap, PF_UNIT};
-  int rc = launch_dispatch(slot_inds, P, S, ws.hist, ws.perm, ws.offsets, ws.inv, &spec, ws.tiles, ws.status, st);
+  int rc = launch_quantize_fp8_hilo(x, T, H, ws.xq_hi, ws.xq_hs, ws.xq_lo, ws.xq_ls, st,
+                                    zero_status ? ws.status : nullptr);
   if (rc) return rc;
-  rc = launch_quantize_fp8_hilo(x, T, H, ws.xq_hi, ws.xq_hs, ws.xq_lo, ws.xq_ls, st);
+  rc = launch_dispatch(slot_inds, P, S, ws.hist, ws.perm, ws.offsets, ws.inv, &spec, ws.tiles, ws.status, st);
   if (rc) return rc;
   PrefillArgs a{};
   a.xq_hi = ws.xq_hi; a.xq_lo = ws.xq_lo; a.xq_hs = ws.xq_hs; a.xq_ls = ws.xq_ls;
@@ -689,8 +690,7 @@ int mimo_moe_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const f
   PrefillWs pw = carve_prefill(c, T, k, bank->n_slots, bank->hidden, bank->inter, 0);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill: workspace too small (need %zu)", c.off);
   if (status_out) pw.status = status_out;
-  reset_status_kernel<<<1, 1, 0, as_stream(stream)>>>(pw.status);
-  return run_prefill(x, T, slot_inds, w, k, bank, nullptr, y, pw, as_stream(stream));
+  return run_prefill(x, T, slot_inds, w, k, bank, nullptr, y, pw, as_stream(stream), true);
 }
 
 int mimo_moe_prefill_staged(const uint16_t* x, int T, const int32_t* slot_inds, const float* w, int k,
@@ -712,8 +712,7 @@ int mimo_moe_prefill_staged(const uint16_t* x, int T, const int32_t* slot_inds, 
   PrefillWs pw = carve_prefill(c, T, k, bank->n_slots + stage->n_slots, bank->hidden, bank->inter, 0);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_prefill_staged: workspace too small (need %zu)", c.off);
   if (status_out) pw.status = status_out;
-  reset_status_kernel<<<1, 1, 0, as_stream(stream)>>>(pw.status);
-  return run_prefill(x, T, slot_inds, w, k, bank, stage, y, pw, as_stream(stream));
+  return run_prefill(x, T, slot_inds, w, k, bank, stage, y, pw, as_stream(stream), true);
 }
 
 size_t mimo_moe_prefill_block_workspace_size(int T, int E, int k, int n_slots, int H, int I) {
@@ -741,13 +740,12 @@ static int prefill_block_impl(const uint16_t* x, int T, const uint16_t* Wg, cons
   int32_t* inds = inds_out ? inds_out : pw.inds;
   float* wts = w_out ? w_out : pw.w;
   if (status_out) pw.status = status_out;
-  reset_status_kernel<<<1, 1, 0, st>>>(pw.status);
-  rc = launch_router_logits(x, Wg, T, bank->hidden, E, pw.logits, st);
+  rc = launch_router_logits(x, Wg, T, bank->hidden, E, pw.logits, st, pw.status);   // clears the status word
   if (rc) return rc;
   rc = launch_router_select(pw.logits, bias, T, E, k, 1.0f, inds, wts, slot_of, pw.slot_inds, bank->n_slots, pw.status,
                             st);
   if (rc) return rc;
-  return run_prefill(x, T, pw.slot_inds, wts, k, bank, nullptr, y, pw, st, resid);
+  return run_prefill(x, T, pw.slot_inds, wts, k, bank, nullptr, y, pw, st, false, resid);
 }
 }  // namespace mimo
 

@@ -40,7 +40,9 @@ int launch_select_group(const float* scores, const float* keys, int T, int E, in
                         int n_slots, int Umax, int32_t* inds_out, float* w_out, int32_t* uids, int32_t* urows,
                         int32_t* ucnt, float* uw, uint32_t* gidx, int32_t* n_unique, int32_t* status,
                         hipStream_t st);
-int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st);
+// zero_status (optional): a status word the launch clears (its first block), for the kernels queued after it
+int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st,
+                         int32_t* zero_status = nullptr);
 int launch_router_select(const float* logits, const float* bias, int T, int E, int k, float scaling, int32_t* inds,
                          float* w, const int32_t* slot_of, int32_t* slot_inds, int n_slots, int32_t* status,
                          hipStream_t st);
@@ -55,6 +57,6 @@ int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int
                     int32_t* inv, const TileSpec* spec, int4* tiles, int32_t* status, hipStream_t st);
 size_t dispatch_workspace(int n, int n_slots);
 int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint8_t* hi, uint8_t* hs, uint8_t* lo,
-                             uint8_t* ls, hipStream_t st);
+                             uint8_t* ls, hipStream_t st, int32_t* zero_status = nullptr);
 
 }  // namespace mimo

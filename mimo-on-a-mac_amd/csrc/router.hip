@@ -243,7 +243,9 @@ int launch_select_group(const float* scores, const float* keys, int T, int E, in
 // ------------------------------------------------------------------ general-T logits: tiled fp32 GEMM
 // logits[t, e] = sum_h x[t, h] * W[e, h]; block tile 32 tokens x 64 experts, K chunks of 64 through LDS.
 __global__ void __launch_bounds__(256) router_logits_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ W,
-                                                            int T, int H, int E, float* __restrict__ logits) {
+                                                            int T, int H, int E, float* __restrict__ logits,
+                                                            int32_t* zero_status) {
+  if (zero_status && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *zero_status = 0;
   __shared__ float xs[32][65];
   __shared__ float ws[64][65];
   const int t0 = blockIdx.y * 32, e0 = blockIdx.x * 64;
@@ -420,18 +422,40 @@ __global__ void __launch_bounds__(1024) dispatch_hist_kernel(const int32_t* __re
   for (int s = threadIdx.x; s < n_slots; s += blockDim.x) hist[(size_t)blockIdx.x * n_slots + s] = h[s];
 }
 
-// offsets[s] = exclusive scan of per-slot totals; base[b][s] = offsets[s] + sum_{b' < b} hist[b'][s]; with a
-// TileSpec, the row tiles of each slot (see TileSpec).  One thread per slot (n_slots <= 1024), wave scans.
-__global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int n_slots,
-                                                             int32_t* __restrict__ offsets, TileSpec spec,
-                                                             int4* __restrict__ tiles) {
+// Scan and placement in one launch: block b (one per chunk) sums the chunk histograms per slot (one thread per
+// slot, n_slots <= 1024), scans the totals over the slots (wave scans), and places its chunk's routes at
+// offsets[s] + sum_{b' < b} hist[b'][s] + (rank among the chunk's routes of slot s).  Block 0 also writes
+// offsets and, with a TileSpec, the row tiles of each slot (see TileSpec).  Ranks within the chunk: earlier
+// waves' counts of the slot (per-wave counts in LDS) plus earlier lanes of the wave (ballots over the slot bits).
+__global__ void __launch_bounds__(1024) dispatch_scan_place_kernel(const int32_t* __restrict__ slots, int n,
+                                                                   const int32_t* __restrict__ hist, int nchunks,
+                                                                   int n_slots, int32_t* __restrict__ offsets,
+                                                                   TileSpec spec, int4* __restrict__ tiles,
+                                                                   int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+  extern __shared__ int dsp[];                   // base[n_slots], then wc[16 waves][n_slots] (counts <= 64)
+  int* base = dsp;
+  uint16_t* wc = reinterpret_cast<uint16_t*>(dsp + n_slots);
   __shared__ int wsum[3][16];
-  const int s = threadIdx.x, lane = s & 63, wv = s >> 6;
-  int c = 0;
-  if (s < n_slots)
-    for (int b = 0; b < nchunks; ++b) c += hist[(size_t)b * n_slots + s];
-  const int nw = (tiles && c > spec.narrow_max) ? (c + spec.wide_rows - 1) / spec.wide_rows : 0;
-  const int ns = (tiles && c >= 1 && c <= spec.narrow_max) ? 1 : 0;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int blk = blockIdx.x;
+  for (int i = tid; i < 16 * n_slots; i += blockDim.x) wc[i] = 0;
+  // per-slot total and the part of it in earlier chunks (integer sums: any order)
+  constexpr int HB = 16;
+  int c = 0, pre = 0;
+  if (tid < n_slots)
+    for (int b0 = 0; b0 < nchunks; b0 += HB) {
+      int h[HB];
+#pragma unroll
+      for (int u = 0; u < HB; ++u) h[u] = b0 + u < nchunks ? hist[(size_t)(b0 + u) * n_slots + tid] : 0;
+#pragma unroll
+      for (int u = 0; u < HB; ++u) {
+        c += h[u];
+        pre += b0 + u < blk ? h[u] : 0;
+      }
+    }
+  const bool tl = tiles != nullptr && blk == 0;
+  const int nw = (tl && c > spec.narrow_max) ? (c + spec.wide_rows - 1) / spec.wide_rows : 0;
+  const int ns = (tl && c >= 1 && c <= spec.narrow_max) ? 1 : 0;
   int v0 = c, v1 = nw, v2 = ns;                  // inclusive scans within the wave
   for (int d = 1; d < 64; d <<= 1) {
     const int u0 = __shfl_up(v0, d, 64), u1 = __shfl_up(v1, d, 64), u2 = __shfl_up(v2, d, 64);
@@ -452,52 +476,42 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(int32_t* __restrict
     v1 += wsum[1][w];
     v2 += wsum[2][w];
   }
-  if (s >= n_slots) return;
-  const int e0 = v0 - c, e1 = v1 - nw, e2 = v2 - ns;   // exclusive prefixes
-  offsets[s] = e0;
-  if (s == n_slots - 1) {
-    offsets[n_slots] = v0;
-    if (tiles) tiles[0] = make_int4(v1, v2, 0, 0);
-  }
-  if (nw) {
-    const int chunks = (c + spec.unit - 1) / spec.unit;
-    for (int q = 0; q < nw; ++q) {
-      const int c0 = (int)((int64_t)q * chunks / nw), c1 = (int)((int64_t)(q + 1) * chunks / nw);
-      tiles[1 + e1 + q] = make_int4(s, e0 + spec.unit * c0, e0 + min(spec.unit * c1, c), 0);
+  if (tid < n_slots) {
+    const int e0 = v0 - c, e1 = v1 - nw, e2 = v2 - ns;   // exclusive prefixes
+    base[tid] = e0 + pre;
+    if (blk == 0) {
+      offsets[tid] = e0;
+      if (tid == n_slots - 1) {
+        offsets[n_slots] = v0;
+        if (tiles) tiles[0] = make_int4(v1, v2, 0, 0);
+      }
+      if (nw) {
+        const int chunks = (c + spec.unit - 1) / spec.unit;
+        for (int q = 0; q < nw; ++q) {
+          const int c0 = (int)((int64_t)q * chunks / nw), c1 = (int)((int64_t)(q + 1) * chunks / nw);
+          tiles[1 + e1 + q] = make_int4(tid, e0 + spec.unit * c0, e0 + min(spec.unit * c1, c), 0);
+        }
+      }
+      if (ns) tiles[1 + spec.wcap + e2] = make_int4(tid, e0, e0 + c, 0);
     }
   }
-  if (ns) tiles[1 + spec.wcap + e2] = make_int4(s, e0, e0 + c, 0);
-  int acc = e0;
-  for (int b = 0; b < nchunks; ++b) {
-    const int h = hist[(size_t)b * n_slots + s];
-    hist[(size_t)b * n_slots + s] = acc;
-    acc += h;
+  // placement of this chunk's routes (slot ids were range-checked and flagged by dispatch_hist_kernel; clamped
+  // identically here)
+  const int i = blk * DISPATCH_CHUNK + tid;
+  const int sl = i < n ? checked_slot(slots, i, n_slots, nullptr) : -1;
+  uint64_t same = __ballot(sl >= 0);
+#pragma unroll
+  for (int bit = 0; bit < 10; ++bit) {           // lanes whose slot agrees with this lane's in every bit
+    const uint64_t ones = __ballot(sl >= 0 && ((sl >> bit) & 1));
+    same &= ((sl >> bit) & 1) ? ones : ~ones;
   }
-}
-
-// stable placement: rank within the chunk = (earlier waves' count of the slot) + (earlier lanes of the wave)
-__global__ void __launch_bounds__(1024) dispatch_place_kernel(const int32_t* __restrict__ slots, int n, int n_slots,
-                                                              const int32_t* __restrict__ base,
-                                                              int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
-  // slot ids were range-checked (and flagged) by dispatch_hist_kernel; clamp identically here
-  extern __shared__ int wc[];     // [16 waves][n_slots]
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < 16 * n_slots; i += blockDim.x) wc[i] = 0;
+  const int lower = __popcll(same & ((1ull << lane) - 1));
+  if (sl >= 0 && lower == 0) wc[wv * n_slots + sl] = (uint16_t)__popcll(same);   // the slot's first lane records
   __syncthreads();
-  int i = blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
-  int s = i < n ? checked_slot(slots, i, n_slots, nullptr) : -1;
-  int lower = 0, same = 0;
-  for (int l = 0; l < 64; ++l) {
-    int o = __shfl(s, l, 64);
-    lower += (l < lane && o == s) ? 1 : 0;
-    same += (o == s) ? 1 : 0;
-  }
-  if (s >= 0 && lower == 0) wc[wave * n_slots + s] = same;   // first lane of each slot records the count
-  __syncthreads();
-  if (s >= 0) {
+  if (sl >= 0) {
     int before = 0;
-    for (int w = 0; w < wave; ++w) before += wc[w * n_slots + s];
-    int pos = base[(size_t)blockIdx.x * n_slots + s] + before + lower;
+    for (int w = 0; w < wv; ++w) before += wc[w * n_slots + sl];
+    const int pos = base[sl] + before + lower;
     perm[pos] = i;
     if (inv) inv[i] = pos;
   }
@@ -510,10 +524,8 @@ int launch_dispatch(const int32_t* slots, int n, int n_slots, int32_t* hist, int
   ProfScope p(st, "prefill_dispatch");
   dispatch_hist_kernel<<<nchunks, 1024, n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, status);
   const TileSpec none{0, 1, 0, 1};
-  dispatch_scan_kernel<<<1, 1024, 0, st>>>(hist, nchunks, n_slots, offsets, spec ? *spec : none,
-                                            spec ? tiles : nullptr);
-  if (n > 0)
-    dispatch_place_kernel<<<nchunks, 1024, 16 * n_slots * sizeof(int), st>>>(slots, n, n_slots, hist, perm, inv);
+  dispatch_scan_place_kernel<<<nchunks, 1024, n_slots * (sizeof(int) + 16 * sizeof(uint16_t)), st>>>(
+      slots, n, hist, nchunks, n_slots, offsets, spec ? *spec : none, spec ? tiles : nullptr, perm, inv);
   return check_launch("prefill dispatch");
 }
 
@@ -550,7 +562,8 @@ constexpr int kRlTok = 32, kRlExp = 64, kRlSplit = 8;
 
 __global__ void __launch_bounds__(512) router_logits_mfma_kernel(const uint16_t* __restrict__ x,
                                                                  const uint16_t* __restrict__ W, int T, int H, int E,
-                                                                 float* __restrict__ logits) {
+                                                                 float* __restrict__ logits, int32_t* zero_status) {
+  if (zero_status && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *zero_status = 0;
   __shared__ float part[kRlSplit][kRlTok][kRlExp];   // 64 KB
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -621,14 +634,15 @@ __global__ void __launch_bounds__(512) router_logits_mfma_kernel(const uint16_t*
   }
 }
 
-int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st) {
+int launch_router_logits(const uint16_t* x, const uint16_t* W, int T, int H, int E, float* logits, hipStream_t st,
+                         int32_t* zero_status) {
   ProfScope p(st, "router_logits");
   if (H % (kRlSplit * 32) == 0 && aligned16(x) && aligned16(W)) {
     dim3 grid((E + kRlExp - 1) / kRlExp, (T + kRlTok - 1) / kRlTok);
-    router_logits_mfma_kernel<<<grid, 512, 0, st>>>(x, W, T, H, E, logits);
+    router_logits_mfma_kernel<<<grid, 512, 0, st>>>(x, W, T, H, E, logits, zero_status);
   } else {
     dim3 grid((E + 63) / 64, (T + 31) / 32);
-    router_logits_kernel<<<grid, 256, 0, st>>>(x, W, T, H, E, logits);
+    router_logits_kernel<<<grid, 256, 0, st>>>(x, W, T, H, E, logits, zero_status);
   }
   return check_launch("router_logits");
 }
