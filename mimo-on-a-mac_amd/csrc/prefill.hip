@@ -105,8 +105,10 @@ __device__ __forceinline__ void pf_wait(int n) {
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
   }
 }
-// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N), 16 bytes each (the words of 4 sub-steps).  An
-// MFMA's scale reads (16 consecutive rows, one word each) fall in 16 distinct banks.
+// Epoch buffer rows: A hi [0, R), A lo [R, 2R), B [2R, 2R + N), 16 bytes each (the words of 4 sub-steps).  Row q
+// keeps sub-step k's word at position k ^ pf_swz(q): without it the MFMAs' byte-wide scale reads conflicted
+// (0.27 conflicts per LDS access in the wide launches against 0.03 with it, on the bank-conflict counter).
+__device__ __forceinline__ int pf_swz(int q) { return (q >> 3) & 3; }
 #define PF_MFMA(A, B, C, SA, SB) __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((A), (B), (C), 0, 4, 0, (SA), 0, (SB))
 
 // One (row tile, output block).  GATEUP: A = the routes' token activations, B = gate rows [0, N/2) and up rows
@@ -172,12 +174,14 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
   // each epoch rather than kept: a route row's from its token in s_tok, a weight row's as a wave-uniform part
   // plus the lane's row.
   static_assert(EP == 4 && R % 16 == 0 && HALF % 16 == 0, "16-byte epoch rows, 16-row copies");
-  const uint32_t e_k4 = 4u * (uint32_t)(lane % EP);   // the lane's word: sub-step lane % EP of the epoch
   auto issue_epoch = [&](int e) __attribute__((always_inline)) {
     uint8_t* dst = pl + PF_SC + (e & 1) * SCB;
-    // words past the row's end read the row's first word instead; they are never used
-    const uint32_t kk = 4u * EP * (uint32_t)e + e_k4;
-    const uint32_t word = kk < (uint32_t)KS ? kk : 0u;
+    // the lane's word of row q: sub-step (lane % EP) ^ pf_swz(q) of the epoch; words past the row's end read
+    // the row's first word instead (they are never used)
+    auto wsw = [&](int q) {
+      const uint32_t kk = 4u * EP * (uint32_t)e + 4u * (uint32_t)((lane % EP) ^ pf_swz(q));
+      return kk < (uint32_t)KS ? kk : 0u;
+    };
 #pragma unroll
     for (int c = 0; c < Sh::ECOP; ++c) {
       const int cc = Sh::ECOP * wave + c;        // wave-uniform
@@ -185,14 +189,15 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
       const int q0 = (64 / EP) * cc;
       if (q0 < 2 * R) {
         const int r = (q0 < R ? q0 : q0 - R) + lane / EP;
-        lds_copy4(q0 < R ? a_hs : a_ls, (uint32_t)s_tok[r < nvalid ? r : 0] * (uint32_t)KS + word, dst + 256 * cc);
+        lds_copy4(q0 < R ? a_hs : a_ls, (uint32_t)s_tok[r < nvalid ? r : 0] * (uint32_t)KS + wsw(q0 + lane / EP),
+                  dst + 256 * cc);
       } else if (q0 < 2 * R + N) {
         const int br0 = q0 - 2 * R;
         const bool up = GATEUP && br0 >= HALF;
-        lds_copy4(up ? us_base : bs_base, (uint32_t)(br0 - (up ? HALF : 0) + lane / EP) * (uint32_t)KS + word,
-                  dst + 256 * cc);
+        lds_copy4(up ? us_base : bs_base,
+                  (uint32_t)(br0 - (up ? HALF : 0) + lane / EP) * (uint32_t)KS + wsw(q0 + lane / EP), dst + 256 * cc);
       } else {
-        lds_copy4(bs_base, word, dst + 256 * cc);   // padding rows of the buffer: never read
+        lds_copy4(bs_base, wsw(0), dst + 256 * cc);   // padding rows of the buffer: never read
       }
     }
   };
@@ -275,7 +280,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
         const uint4 v = *reinterpret_cast<const uint4*>(st + Sh::B_OFF + brow0 * (64 * Sh::KSUB) + bslot[u] +
                                                         bdt(t) * (64 * Sh::KSUB));
         B[t] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
-        sb[t] = sc[bsc0 + 4 * kw + 4 * EP * bdt(t)];
+        sb[t] = sc[bsc0 + 4 * (kw ^ pf_swz(2 * R + brow0 + bdt(t))) + 4 * EP * bdt(t)];
       }
       v8i A[NJ][2];
       int sa[NJ][2];
@@ -287,7 +292,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
           const uint4 lo16 = *reinterpret_cast<const uint4*>(ab + sw_lo);
           const uint4 hi16 = *reinterpret_cast<const uint4*>(ab + sw_hi);
           A[j][p] = v8i{(int)lo16.x, (int)lo16.y, (int)lo16.z, (int)lo16.w, (int)hi16.x, (int)hi16.y, (int)hi16.z, (int)hi16.w};
-          sa[j][p] = sc[asc[j][p] + 4 * kw];
+          sa[j][p] = sc[asc[j][p] + 4 * (kw ^ pf_swz(p * R + PF_UNIT * (cb + Sh::CSTEP * j) + i))];
         }
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
