@@ -80,8 +80,11 @@ def test_group_routes_slot_table_and_overflow(rng):
         group_routes(bad, scores, R=8, slot_of=slot_of, n_slots=16)
 
 
-@pytest.mark.parametrize("T,S,k", [(512, 256, 8), (2048, 256, 8), (4096, 256, 8), (5, 8, 2), (1, 256, 8)])
+@pytest.mark.parametrize("T,S,k", [(512, 256, 8), (2048, 256, 8), (4096, 256, 8), (5, 8, 2), (1, 256, 8),
+                                   (300, 1024, 8), (1000, 1000, 3), (3000, 512, 8)])
 def test_prefill_dispatch_bit_exact(rng, T, S, k):
+    """Stable counting sort against the oracle; the last three cases take the largest slot count (1024), a slot
+    count that is not a power of two and ragged chunks (T * k not a multiple of the 1024-route chunk)."""
     from mimo_stream import prefill_dispatch
     slots = zipf_routes(rng, T, S, k)
     perm, offsets, inv = prefill_dispatch(torch.from_numpy(slots).cuda(), S)
