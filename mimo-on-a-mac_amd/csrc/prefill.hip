@@ -83,7 +83,7 @@ template <bool W> constexpr int pf_lds_bytes() {
   using Sh = PfShape<W>;
   static_assert(Sh::B_OFF == Sh::KSUB * 2 * Sh::A_PL && Sh::B_OFF + Sh::N * 64 * Sh::KSUB <= Sh::STAGE &&
                     2 * Sh::R + Sh::N <= Sh::SC_ROWS, "stage layout");
-  static_assert(Sh::TGW * 64 == Sh::N && 8 * Sh::NJ * 16 >= Sh::TGW * Sh::R && Sh::BCOP * 128 == Sh::N * Sh::KSUB,
+  static_assert(Sh::TGW * 64 == Sh::N && 8 * Sh::NJ * 16 == Sh::TGW * Sh::R && Sh::BCOP * 128 == Sh::N * Sh::KSUB,
                 "wave roles");
   static_assert(Sh::EPOCH % Sh::KSUB == 0 && Sh::EPOCH / Sh::KSUB >= Sh::STAGES - 1, "epoch buffers reused in time");
   static_assert(Sh::SC_ROWS * 4 * Sh::EPOCH == 256 * Sh::NCOPY && 8 * Sh::ECOP >= Sh::NCOPY, "epoch copies");
@@ -219,13 +219,11 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
 
   // the wave's tiles: weight rows 64 tg .. (GATEUP t = 2 p + b: projection p, 16-output half b), chunks
   // cb + CSTEP j (routes 16 chunk ..) for the live j
-  // (the narrow shape has MFMA work for 4 of its 8 waves; the others only copy)
   const int tg = wave % Sh::TGW;
   const int cb = wave / Sh::TGW;
-  constexpr int MWAVES = Sh::TGW * (R / PF_UNIT) / NJ;
   uint32_t live = 0;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) live |= (wave < MWAVES && PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
+  for (int j = 0; j < NJ; ++j) live |= (PF_UNIT * (cb + Sh::CSTEP * j) < nvalid) ? 1u << j : 0u;
   live = __builtin_amdgcn_readfirstlane(live);
   // row of tile t = brow0 + bdt(t), bdt a compile-time constant, so the tiles' LDS addresses share one register
   auto bdt = [](int t) constexpr { return GATEUP ? (t >> 1) * HALF + 16 * (t & 1) : 16 * t; };
@@ -268,7 +266,7 @@ __device__ __forceinline__ void pf_tile(const PrefillArgs& a, uint8_t* pl, int* 
     const uint8_t* st = pl + (s % Sh::STAGES) * Sh::STAGE;
 #pragma unroll
     for (int u = 0; u < Sh::KSUB; ++u) {
-      if (!live) break;                          // wave-uniform: a wave without live chunks only copies
+      if (!live) break;                          // wave-uniform: no chunk of this wave holds routes
       const int ss = Sh::KSUB * s + u;           // sub-step: 128 codes
       const uint8_t* sc = pl + PF_SC + ((ss / EP) & 1) * SCB;
       const int kw = ss % EP;
