@@ -503,7 +503,7 @@ struct PrefillWs {
 struct PfTiling {
   int narrow_max, wcap, scap;
 };
-static PfTiling pf_tiling(int64_t P, int S, int H, int I) {
+static PfTiling pf_tiling(int64_t P, int S, int I) {
   PfTiling t;
   const bool narrow = I % 256 == 0;    // narrow blocks: 128 (gate/up) or 256 (down) outputs, K-steps of 256
   t.narrow_max = narrow ? PF_NARROW_MAX : 0;
@@ -515,7 +515,7 @@ static PfTiling pf_tiling(int64_t P, int S, int H, int I) {
 static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int E) {
   PrefillWs w{};
   const size_t P = (size_t)T * k;
-  const PfTiling tl = pf_tiling((int64_t)P, S, H, I);
+  const PfTiling tl = pf_tiling((int64_t)P, S, I);
   w.status = c.take<int32_t>(1);
   w.hist = reinterpret_cast<int32_t*>(c.take<char>(dispatch_workspace((int)P, S)));
   w.perm = c.take<int32_t>(P);
@@ -593,7 +593,7 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   int err;
   const uint16_t* sig = sigtab_device(&err);
   if (!sig) return err;
-  const PfTiling tl = pf_tiling(P, S, H, I);
+  const PfTiling tl = pf_tiling(P, S, I);
   const TileSpec spec{tl.narrow_max, PF_WIDE_ROWS, tl.wcap, PF_UNIT};
   int rc = launch_quantize_fp8_hilo(x, T, H, ws.xq_hi, ws.xq_hs, ws.xq_lo, ws.xq_ls, st,
                                     zero_status ? ws.status : nullptr);

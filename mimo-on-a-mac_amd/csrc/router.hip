@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
     }
   }
   __syncthreads();
-  if (threadIdx.x < a.T) {          // one thread per row: the four quarters in order, sigmoid and selection key
+  if ((int)threadIdx.x < a.T) {     // one thread per row: the four quarters in order, sigmoid and selection key
     const int r = threadIdx.x;
     const float l = ((part[r][0] + part[r][1]) + part[r][2]) + part[r][3];
     const float s = sigmoid_spec(l);

@@ -43,8 +43,8 @@ __device__ __forceinline__ void wave_select_set(const uint32_t (&cv)[PER], int k
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint64_t tie = __ballot(cv[j] == T);
-    take[j] = cv[j] > T || (cv[j] == T && ties_before + __popcll(tie & below) < need);
-    ties_before += __popcll(tie);
+    take[j] = cv[j] > T || (cv[j] == T && ties_before + (int)__popcll(tie & below) < need);
+    ties_before += (int)__popcll(tie);
   }
 }
 
