@@ -676,7 +676,7 @@ def main():
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the MoE block runs on a single MI355X "
+        print(json.dumps({"error": "bench.py measures one GPU only: the MoE block runs on a single MI355X "
                                    "(multi-GPU sharding is designed, not implemented)",
                           "n_gpus": args.gpus}))
         sys.exit(2)

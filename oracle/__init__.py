@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  This package restates, in numpy, the algorithm of the reference engine's MoE
 block (engine/mimo_stream/kernels.py, engine/mimo_stream/model.py:26-65, :173-271, engine/mimo_stream/cache.py,
-engine/mimo_stream/mimo_v2.py:165-239).  It is the checker the HIP implementation is compared against, and the
+engine/mimo_stream/mimo_v2.py:165-239).  It is the oracle the HIP implementation is compared against, and the
 timed CPU baseline in bench.py.  Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may
 import it; the product path (mimo_stream + libmimo_moe.so) never does.
 

@@ -7,7 +7,7 @@ Reference layout: engine/mimo_stream/kernels.py:5-12 and scripts/convert-mimo-v2
 Decode (engine/mimo_stream/kernels.py:19-30): e2m1(c) in {+-0, .5, 1, 1.5, 2, 3, 4, 6};
 e8m0(s) = 2^(s-127) with s=0 -> 2^-127 and s=255 -> NaN.
 
-The quantisers here are this build's own (the reference's mx.quantize is third-party MLX and only makes test
+The quantisers here are written from the OCP specification (the reference's mx.quantize is third-party MLX and only makes test
 data: both sides of every parity check consume the same packed bytes).  quantize_mxfp4 follows the OCP
 Microscaling v1.0 rule (shared exponent floor(log2(amax)) - 2, round-to-nearest-even onto the E2M1 grid,
 saturate at 6).  quantize_fp8_hilo is the activation split used by the block-scaled MFMA paths: a bf16 value
