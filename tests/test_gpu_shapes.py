@@ -2,7 +2,8 @@
 ragged token counts, against the oracle (decode: the distinct-expert path and the M = 1 gather path;
 prefill: the grouped GEMMs and combine).  Decode takes hidden sizes 256-4096 (powers of two) and intermediate
 sizes 512, 1024 or 2048; prefill any hidden size that is a multiple of 256 and intermediate size that is a
-multiple of 128 (the 512-row narrow tiles only when the outputs divide into them, wide tiles otherwise).
+multiple of 128 (narrow tiles of rarely chosen experts only when the intermediate size is a multiple of 256, whose
+K-steps of 256 codes the down GEMM then divides into; every tile wide otherwise).
 The bar is the one of the other parity tests."""
 import numpy as np
 import pytest
