@@ -7,10 +7,11 @@ hidden 256, intermediate 512):
             routes bit-exact given the logits, y against the oracle on a sub-pool of the selected experts.
   rows      the same layer at 2, 4 and 8 rows with routing steered so consecutive rows share experts (the
             distinct-expert kernels, kernels.py:176-199).
-  prefill   Zipf(1.1) routes at 512, 2048 and 4096 tokens (4096 = the reference server's chunk,
-            engine/server.py:34: 32,768 slot-sorted routes, the size bench/scripts/gather_qmm_sorted_check.py:36
-            checks).  Every token is compared: the combine weights are nonzero only on routes to a set Q of up to
-            16 experts spread over the popularity ranks (the most popular one, cut into many 96-route tiles, down
+  prefill   Zipf(1.1) routes at 512, 2048, 4096, 5001 and 6250 tokens (4096 = the reference server's chunk,
+            engine/server.py:34: 32,768 slot-sorted routes; 40,008 and 50,000 routes past 32,767 and off multiples
+            of 64, the row counts bench/scripts/gather_qmm_sorted_check.py:36 checks).  Every token is compared:
+            the combine weights are nonzero only on routes to a set Q of up to 16 experts spread over the
+            popularity ranks (the most popular one, cut into many 64-route tiles, down
             to experts with a single route), so the oracle needs only Q's weights while every tile of those
             experts, both tile shapes and multi-term combines are checked; tokens with no route into Q must come
             out exactly zero.  A second call with every weight nonzero is compared on 4 random tokens.
