@@ -15,6 +15,7 @@
 //   FP8 operand: bytes 0-15 hold K = 16g .. 16g+15, bytes 16-31 hold K = 64+16g .. 64+16g+15.
 //   scale of K-block b (32 wide) of row/column i comes from lane i + 16b (byte 0).
 //   D: lane l holds column l % 16, rows 4g .. 4g+3.
+#include <atomic>
 #include <mutex>
 
 #include "device.h"
@@ -656,19 +657,23 @@ static int check_bank(const mimo_bank* b) {
   return MIMO_OK;
 }
 
-// Dynamic LDS above the default 64 KB has to be allowed per kernel once.
-static int allow_lds(const void* fn, size_t bytes, int* allowed) {
-  if ((int)bytes <= 65536 || (int)bytes <= *allowed) return MIMO_OK;
+// Dynamic LDS above the default 64 KB has to be allowed per kernel once.  `allowed` (the largest size set so far)
+// is read without a lock; raising it is serialised, so the attribute never drops below a size already allowed.
+static std::mutex g_lds_attr_mu;
+static int allow_lds(const void* fn, size_t bytes, std::atomic<int>* allowed) {
+  if ((int)bytes <= 65536 || (int)bytes <= allowed->load(std::memory_order_acquire)) return MIMO_OK;
+  std::lock_guard<std::mutex> lk(g_lds_attr_mu);
+  if ((int)bytes <= allowed->load(std::memory_order_relaxed)) return MIMO_OK;
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   if (e != hipSuccess)
     return set_error(MIMO_ERR_HIP, "hipFuncSetAttribute(%zu bytes of LDS): %s", bytes, hipGetErrorString(e));
-  *allowed = (int)bytes;
+  allowed->store((int)bytes, std::memory_order_release);
   return MIMO_OK;
 }
 
 template <int NS, bool ROUTED, bool FAST2>
 static int launch_gateup(const ExpertsArgs& a, int rl, hipStream_t st) {
-  static int allowed = 0;
+  static std::atomic<int> allowed{0};
   const size_t lds = (size_t)gateup_lds(a.H, rl).total;
   int rc = allow_lds(reinterpret_cast<const void*>(&decode_gateup_kernel<NS, ROUTED, FAST2>), lds, &allowed);
   if (rc) return rc;
@@ -678,7 +683,7 @@ static int launch_gateup(const ExpertsArgs& a, int rl, hipStream_t st) {
 
 template <int NS>
 static int launch_down(const ExpertsArgs& a, int rw, hipStream_t st) {
-  static int allowed = 0;
+  static std::atomic<int> allowed{0};
   const size_t lds = (size_t)down_lds(a.I, rw, a.M * a.k).total;
   int rc = allow_lds(reinterpret_cast<const void*>(&decode_down_combine_kernel<NS>), lds, &allowed);
   if (rc) return rc;

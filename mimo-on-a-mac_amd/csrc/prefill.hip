@@ -14,6 +14,7 @@
 // routes, the block's E2M1 weight rows; E8M0 scales once per epoch); each wave multiplies 16-route chunks by
 // four 16-row weight tiles, the hi and lo planes accumulating into the same tile.  The epilogue stages results in
 // LDS and writes 16-byte pieces.
+#include <atomic>
 #include <mutex>
 
 #include "device.h"
@@ -571,12 +572,12 @@ static SideStream* side_stream() {
 }
 
 template <bool GATEUP, bool WIDE> static int pf_allow_lds() {
-  static int allowed = 0;
-  if (allowed) return MIMO_OK;
+  static std::atomic<int> allowed{0};   // host threads may race to set the attribute; setting it twice is harmless
+  if (allowed.load(std::memory_order_acquire)) return MIMO_OK;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<GATEUP, WIDE>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, pf_lds_bytes<WIDE>());
   if (e != hipSuccess) return set_error(MIMO_ERR_HIP, "prefill LDS attribute: %s", hipGetErrorString(e));
-  allowed = 1;
+  allowed.store(1, std::memory_order_release);
   return MIMO_OK;
 }
 
