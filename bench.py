@@ -307,7 +307,7 @@ def stack_case(layers, M, tokens, device, seed):
             "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-HEADLINE_KERNEL = ("decode_gateup_kernel<8, true, false>", 32768, 8)     # 1-row decode: 64 x 8 blocks of 512
+HEADLINE_KERNEL = ("decode_gateup_kernel<8, true, false, true>", 32768, 8)   # 1-row decode: 128 x 8 blocks of 256
 
 
 def trace_parse(d):

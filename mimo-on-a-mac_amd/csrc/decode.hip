@@ -108,11 +108,11 @@ __host__ __device__ inline GateupLds gateup_lds(int H, int rl) {
 }
 
 // Stage activation rows c0 .. c0 + n - 1 of the block's expert into LDS (rows 0 .. n - 1 there): per row, the
-// hi and lo codes in 1 KB pieces and the [hi | lo] scales in one piece, spread over the block's 8 waves,
-// at most JMAX pieces per wave (n <= 8 rows of H <= 4096 need 9).  Straight-line code: a loop here would
-// make the compiler drain every outstanding load before entering it.
+// hi and lo codes in 1 KB pieces and the [hi | lo] scales in one piece, spread over the block's NW waves,
+// at most JMAX pieces per wave (n <= 8 rows of H <= 4096 need 9 with 8 waves).  Straight-line code: a loop here
+// would make the compiler drain every outstanding load before entering it.
 // tok: lane c holds the token of row c (wave-uniform reads through readlane).
-template <int JMAX>
+template <int JMAX, int NW = 8>
 __device__ __forceinline__ void stage_act_rows(const ExpertsArgs& a, uint8_t* lds, const GateupLds& L, int c0, int n,
                                                int tok, int wave, int lane) {
   const int nq = (a.H + 1023) >> 10;          // 1 KB pieces per half row
@@ -120,7 +120,7 @@ __device__ __forceinline__ void stage_act_rows(const ExpertsArgs& a, uint8_t* ld
   const int hs = a.H / 32;
 #pragma unroll
   for (int j = 0; j < JMAX; ++j) {
-    const int t = wave + 8 * j;
+    const int t = wave + NW * j;
     if (t >= n * per_row) break;
     const int c = t / per_row, p = t - c * per_row;
     int token = __builtin_amdgcn_readlane(tok, c0 + c);
@@ -170,9 +170,16 @@ __device__ __forceinline__ void publish_routes(const ExpertsArgs& a, const int32
   if (tid == 0) { a.rt_nu[0] = g_nu[0]; a.rt_status[0] = g_nu[1]; }
 }
 
-// FAST2 (routed only; the launcher checks its conditions): two rows with expert ids as slots
-template <int NS, bool ROUTED, bool FAST2>
+// FAST2 (routed only; the launcher checks its conditions): two rows with expert ids as slots.
+// HALF (with FAST2): blocks of 256 threads and 16 outputs (wave w: K-range w), four per CU, so that a step's
+// U x I / 16 blocks spread more evenly over the CUs than U x I / 32 larger ones; such a block writes h in bf16
+// and the down kernel splits it (an E8M0 block of h spans 32 outputs, two of these blocks).
+template <int NS, bool ROUTED, bool FAST2, bool HALF = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a, int rl) {
+  static_assert(!HALF || ROUTED, "16-output blocks only for the routed kernel");
+  constexpr int NW = HALF ? 4 : 8;        // waves per block
+  constexpr int NT = HALF ? 1 : 2;        // 16-output tiles per block
+  constexpr int BO = 16 * NT;             // outputs per block
   extern __shared__ __align__(16) uint8_t lds[];
   // routed grouping (ROUTED only): kept for the publication at the end of block (0, 0)
   __shared__ int sel[ROUTED ? 8 : 1][kSelLds];
@@ -259,12 +266,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   wait_vm_all();   // the metadata loads are done; nothing the compiler tracks stays in flight past this point
   const GateupLds L = gateup_lds(a.H, rl);
   // the activation rows go first (they need only the metadata the weight addresses need as well)
-  constexpr int JMAX = ROUTED ? 3 : 9;    // routed batches stage at most 2 rows at once, others 8
-  stage_act_rows<JMAX>(a, lds, L, 0, min(cnt, rl), tok, wave, lane);
+  constexpr int JMAX = ROUTED ? (HALF ? 5 : 3) : 9;   // routed batches stage at most 2 rows at once, others 8
+  stage_act_rows<JMAX, NW>(a, lds, L, 0, min(cnt, rl), tok, wave, lane);
   __builtin_amdgcn_sched_barrier(0);
 
-  const int ntile = wave & 1, kr = wave >> 1;
-  const int nb = blockIdx.x * 32;
+  const int ntile = HALF ? 0 : (wave & 1), kr = HALF ? wave : (wave >> 1);
+  const int nb = blockIdx.x * BO;
   const int n0 = nb + ntile * 16;
   const size_t brow = (size_t)slot * a.I + n0 + i;
   const int ksplit = gateup_ksplit(a.H);
@@ -273,17 +280,18 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   const int b0 = k0 / 32;
   const uint4* gw = reinterpret_cast<const uint4*>(a.gate_w + brow * (a.H / 8)) + b0 + g;   // one uint4 per 32-block
   const uint4* upw = reinterpret_cast<const uint4*>(a.up_w + brow * (a.H / 8)) + b0 + g;
-  // the block's gate and up scales (32 rows x H/32 bytes each, contiguous in the pools) in 8-byte pieces
+  // the block's gate and up scales (BO rows x H/32 bytes each, contiguous in the pools) in 8-byte pieces
+  constexpr int LG_BO = HALF ? 4 : 5;
   const int lg_pr = __builtin_ctz(a.H / 256);             // pieces per scale row = H / 256
-  const int npieces = 64 << lg_pr;
-  const int p0 = tid, p1 = tid + 512;
+  const int npieces = (2 * BO) << lg_pr;
+  const int p0 = tid, p1 = tid + 64 * NW;
   const int q0 = p0 < npieces ? p0 : 0, q1 = p1 < npieces ? p1 : 0;
   auto piece_src = [&](int p) {
-    const int proj = p >> (5 + lg_pr), row = (p >> lg_pr) & 31, c = p & ((1 << lg_pr) - 1);
+    const int proj = p >> (LG_BO + lg_pr), row = (p >> lg_pr) & (BO - 1), c = p & ((1 << lg_pr) - 1);
     return reinterpret_cast<const uint2*>((proj ? a.up_s : a.gate_s) + ((size_t)slot * a.I + nb + row) * (a.H / 32)) + c;
   };
   auto piece_dst = [&](int p) {
-    const int proj = p >> (5 + lg_pr), row = (p >> lg_pr) & 31, c = p & ((1 << lg_pr) - 1);
+    const int proj = p >> (LG_BO + lg_pr), row = (p >> lg_pr) & (BO - 1), c = p & ((1 << lg_pr) - 1);
     return reinterpret_cast<uint2*>(lds + (proj * 32 + row) * L.RS + 8 * c);
   };
   // the scale pieces, then the weight batch: the activation rows and the scales land first, so each MFMA step
@@ -345,7 +353,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   run_pass(0);
   for (int c0 = rl; c0 < cnt; c0 += rl) {   // rare: more rows routed to one expert than staged at once
     __syncthreads();
-    stage_act_rows<JMAX>(a, lds, L, c0, min(cnt - c0, rl), tok, wave, lane);
+    stage_act_rows<JMAX, NW>(a, lds, L, c0, min(cnt - c0, rl), tok, wave, lane);
     wait_vm_all();
     __syncthreads();
     run_pass(c0);
@@ -367,9 +375,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
   __syncthreads();
   // SwiGLU, one (row, output) per thread: K-range partials summed in a fixed order (0, 1, 2, 3)
   uint16_t hb = 0;
-  const int e_q = tid & 3, e_l = (tid >> 2) & 31, e_nt = (tid >> 7) & 1;
+  const int e_q = tid & 3, e_l = (tid >> 2) & 31, e_nt = HALF ? 0 : ((tid >> 7) & 1);
   const int e_r = 4 * (e_l >> 4) + e_q, e_n = e_nt * 16 + (e_l & 15);
-  if (tid < 256) {
+  if (tid < 128 * NT) {
     float gsum = red[0][e_nt][0][e_l][e_q], usum = red[0][e_nt][1][e_l][e_q];
 #pragma unroll
     for (int j = 1; j < 4; ++j) {
@@ -383,7 +391,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) d
     const float sig = round_bf16(sigmoid_spec(gtf));   // the bf16 sigmoid table's entry for gt, computed in place
     const float hv = round_bf16(round_bf16(gtf * sig) * ut);
     hb = e_r < cnt ? f32_to_bf16(hv) : (uint16_t)0;
-    hl[e_r][e_n] = e_r < cnt ? hv : 0.0f;
+    if constexpr (!HALF) hl[e_r][e_n] = e_r < cnt ? hv : 0.0f;
+  }
+  if constexpr (HALF) {            // h in bf16 for the down kernel's split (and the padding rows when asked)
+    if (tid < 128 && (e_r < cnt || (a.zero_pad && e_r < a.R)))
+      a.h[((size_t)u * a.R + e_r) * a.I + nb + e_n] = hb;
+    if (publisher) publish_routes(a, s_inds, s_w, g_uids, g_urows, g_ucnt, g_uw, g_gidx, g_nu, tid);
+    return;
   }
   __syncthreads();
   if (a.zero_pad && tid < 256 && e_r < a.R)   // h itself only for callers that asked for the intermediates
@@ -446,7 +460,10 @@ __host__ __device__ inline DownLds down_lds(int I, int rw, int nroutes) {
   return L;
 }
 
-template <int NS>
+// HSPLIT: h comes in bf16 (from the 16-output gate/up blocks) and each wave splits its item's rows into the hi/lo
+// E4M3 planes itself, one 32-block per lane (rows of the K-half at lanes 0-31 and 32-63, so rw <= 2), while its
+// weights stream; the planes and scales are those the gate/up epilogue writes otherwise.
+template <int NS, bool HSPLIT = false>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) decode_down_combine_kernel(ExpertsArgs a, int rw) {
   extern __shared__ __align__(16) uint8_t dl[];
   __shared__ uint32_t cgidx[64];      // combine indices and weights, loaded with the routing metadata
@@ -494,6 +511,39 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
       else if (4 * lane < 2 * sb) lds_copy4(a.hq_ls + row * (a.I / 32) + kh * sb - sb, 4 * lane, dst);
     }
   };
+  // HSPLIT: lane l holds bf16 values 16 l .. 16 l + 15 of the K-half (block l / 2) of staged rows c0 and c0 + 1
+  auto hload = [&](int u, int kh, int c0, int n, bool active, uint4 (&hv)[2][2]) {
+    const bool live = active && 16 * lane < L.KH;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const size_t row = (size_t)u * a.R + c0 + (c < n ? c : 0);
+      const uint4* hp = reinterpret_cast<const uint4*>(a.h + row * a.I + kh * L.KH + 16 * (live ? lane : 0));
+      hv[c][0] = hp[0];
+      hv[c][1] = hp[1];
+    }
+    return live;
+  };
+  // every lane calls this (the pair exchanges its block maxima); rows c < n of the live lanes are written
+  auto hsplit = [&](const uint4 (&hv)[2][2], int n, bool live) {
+    const int sb = L.KH / 32;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if (c >= n) break;                            // wave-uniform
+      const uint32_t pw[8] = {hv[c][0].x, hv[c][0].y, hv[c][0].z, hv[c][0].w,
+                              hv[c][1].x, hv[c][1].y, hv[c][1].z, hv[c][1].w};
+      uint32_t hw[4], lw[4];
+      int X, Y;
+      quant_pair_fp8_hilo(pw, hw, lw, &X, &Y);
+      if (live) {
+        *reinterpret_cast<uint4*>(wb + L.hi + c * L.RA + 16 * lane) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *reinterpret_cast<uint4*>(wb + L.lo + c * L.RA + 16 * lane) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        if ((lane & 1) == 0) {
+          wb[L.sc + c * 2 * sb + (lane >> 1)] = (uint8_t)(X + 127);
+          wb[L.sc + c * 2 * sb + sb + (lane >> 1)] = (uint8_t)(Y + 127);
+        }
+      }
+    }
+  };
   // scale staging: lane L loads 8 bytes of row L / LPR of the item's K-half (NS * 4 bytes per row)
   constexpr int LPR = NS / 2;
   const int srow = min(lane / LPR, 15), spart = lane % LPR;
@@ -505,7 +555,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     const int slot = __builtin_amdgcn_readlane(slotv, u);
     const int rbase = __builtin_amdgcn_readlane(prefv, u);
     const bool active = cnt > 0 && slot >= 0 && slot < a.S;
-    if (active) stage(u, kh, 0, min(cnt, rw));
+    uint4 hv[2][2];
+    bool hlive = false;
+    if constexpr (HSPLIT) hlive = hload(u, kh, 0, min(cnt, rw), active, hv);
+    else if (active) stage(u, kh, 0, min(cnt, rw));
     const int b0 = kh * NS * 4;      // first 32-block of this K-half
     const size_t bslot = (size_t)(active ? slot : 0) * a.H + m0;
     const uint4* dw = reinterpret_cast<const uint4*>(a.down_w + (bslot + i) * (a.I / 8)) + b0 + g;
@@ -516,6 +569,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     __builtin_amdgcn_sched_barrier(0);   // every weight load is in flight before anything waits
     wait_vm_keep<NS>();                  // the staged rows and the scales have landed; each MFMA step then waits
                                          // only for its own weights
+    if constexpr (HSPLIT) hsplit(hv, min(cnt, rw), hlive);   // while the weights stream
     if (lane < 16 * LPR) *reinterpret_cast<uint2*>(&wsc[wave][srow * SRS + 2 * spart]) = sraw;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
@@ -549,7 +603,14 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) 
     if (active) run_pass(0);
     for (int c0 = rw; active && c0 < cnt; c0 += rw) {   // rare: more rows on one expert than the buffer holds
       __builtin_amdgcn_wave_barrier();
-      stage(u, kh, c0, min(cnt - c0, rw));
+      if constexpr (HSPLIT) {
+        uint4 hv2[2][2];
+        const bool live2 = hload(u, kh, c0, min(cnt - c0, rw), true, hv2);
+        wait_vm_all();
+        hsplit(hv2, min(cnt - c0, rw), live2);
+      } else {
+        stage(u, kh, c0, min(cnt - c0, rw));
+      }
       wait_vm_all();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       __builtin_amdgcn_wave_barrier();
@@ -624,14 +685,15 @@ struct ExpertsWs {
   float* part;
 };
 // intermediates: room for the bf16 h and the fp32 partials, written only when a caller of mimo_moe_experts asks
-// for them (the fused decode never does)
-static ExpertsWs carve_experts(Carve& c, int M, int Umax, int R, int H, int I, bool intermediates) {
+// for them (the fused decode never does); bf16_h: room for h alone (the two-row fused decode passes h in bf16)
+static ExpertsWs carve_experts(Carve& c, int M, int Umax, int R, int H, int I, bool intermediates,
+                               bool bf16_h = false) {
   ExpertsWs w{};
   w.xq_hi = c.take<uint8_t>((size_t)M * H);
   w.xq_lo = c.take<uint8_t>((size_t)M * H);
   w.xq_hs = c.take<uint8_t>((size_t)M * H / 32);
   w.xq_ls = c.take<uint8_t>((size_t)M * H / 32);
-  if (intermediates) w.h = c.take<uint16_t>((size_t)Umax * R * I);
+  if (intermediates || bf16_h) w.h = c.take<uint16_t>((size_t)Umax * R * I);
   w.hq_hi = c.take<uint8_t>((size_t)Umax * R * I);
   w.hq_lo = c.take<uint8_t>((size_t)Umax * R * I);
   w.hq_hs = c.take<uint8_t>((size_t)Umax * R * I / 32);
@@ -681,13 +743,24 @@ static int launch_gateup(const ExpertsArgs& a, int rl, hipStream_t st) {
   return MIMO_OK;
 }
 
-template <int NS>
+template <int NS, bool HSPLIT = false>
 static int launch_down(const ExpertsArgs& a, int rw, hipStream_t st) {
   static std::atomic<int> allowed{0};
   const size_t lds = (size_t)down_lds(a.I, rw, a.M * a.k).total;
-  int rc = allow_lds(reinterpret_cast<const void*>(&decode_down_combine_kernel<NS>), lds, &allowed);
+  int rc = allow_lds(reinterpret_cast<const void*>(&decode_down_combine_kernel<NS, HSPLIT>), lds, &allowed);
   if (rc) return rc;
-  decode_down_combine_kernel<NS><<<a.H / 16, 1024, lds, st>>>(a, rw);
+  decode_down_combine_kernel<NS, HSPLIT><<<a.H / 16, 1024, lds, st>>>(a, rw);
+  return MIMO_OK;
+}
+
+// one or two rows, expert ids as slots: 16-output gate/up blocks (h in bf16), the down kernel splitting h
+template <int NS, bool FAST2>
+static int launch_gateup_half(const ExpertsArgs& a, int rl, hipStream_t st) {
+  static std::atomic<int> allowed{0};
+  const size_t lds = (size_t)gateup_lds(a.H, rl).total;
+  int rc = allow_lds(reinterpret_cast<const void*>(&decode_gateup_kernel<NS, true, FAST2, true>), lds, &allowed);
+  if (rc) return rc;
+  decode_gateup_kernel<NS, true, FAST2, true><<<dim3(a.I / 16, a.Umax), 256, lds, st>>>(a, rl);
   return MIMO_OK;
 }
 
@@ -706,12 +779,26 @@ static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream
     if (rc) return rc;
   }
   int rc;
+  bool half = false;   // 16-output gate/up blocks, h split by the down kernel
   {
     ProfScope p(st, "decode_gateup");
     // two rows with expert ids as slots (E <= 256 for a fused selection): each block finds its own expert from
     // the two threshold searches alone (one row does the same inside the general routed kernel)
     const bool fast2 = fused_select && a.slot_of == nullptr && a.S >= a.E && M == 2;
-    if (fused_select) {   // cheaper than a separate selection launch
+    const bool fast1 = fused_select && a.slot_of == nullptr && a.S >= a.E && M == 1;
+    half = (fast1 || fast2) && a.h != nullptr && rw <= 2 && !a.zero_pad;
+    if (half) {
+      switch (ns * 2 + (fast2 ? 1 : 0)) {
+        case 17: rc = launch_gateup_half<8, true>(a, rl, st); break;
+        case 16: rc = launch_gateup_half<8, false>(a, rl, st); break;
+        case 9: rc = launch_gateup_half<4, true>(a, rl, st); break;
+        case 8: rc = launch_gateup_half<4, false>(a, rl, st); break;
+        case 5: rc = launch_gateup_half<2, true>(a, rl, st); break;
+        case 4: rc = launch_gateup_half<2, false>(a, rl, st); break;
+        case 3: rc = launch_gateup_half<1, true>(a, rl, st); break;
+        default: rc = launch_gateup_half<1, false>(a, rl, st); break;
+      }
+    } else if (fused_select) {   // cheaper than a separate selection launch
       switch (ns * 2 + (fast2 ? 1 : 0)) {
         case 17: rc = launch_gateup<8, true, true>(a, rl, st); break;
         case 16: rc = launch_gateup<8, true, false>(a, rl, st); break;
@@ -734,7 +821,10 @@ static int run_experts(const ExpertsArgs& base, int M, int round_bf16, hipStream
   if (rc) return rc;
   {
     ProfScope p(st, "decode_down_combine");
-    switch (a.I / 256) {
+    switch (a.I / 256 + (half ? 16 : 0)) {
+      case 24: rc = launch_down<8, true>(a, rw, st); break;
+      case 20: rc = launch_down<4, true>(a, rw, st); break;
+      case 18: rc = launch_down<2, true>(a, rw, st); break;
       case 8: rc = launch_down<8>(a, rw, st); break;
       case 4: rc = launch_down<4>(a, rw, st); break;
       default: rc = launch_down<2>(a, rw, st); break;
@@ -819,7 +909,7 @@ size_t mimo_moe_decode_workspace_size(int M, int E, int k, int H, int I) {
   int32_t *inds, *uids, *urows, *ucnt, *nu, *st;
   uint32_t* gidx;
   carve_decode(c, M, E, k, Umax, kDecodeR, &l, &s, &kk, &inds, &w, &uids, &urows, &ucnt, &uw, &gidx, &nu, &st);
-  carve_experts(c, M, Umax, kDecodeR, H, I, false);
+  carve_experts(c, M, Umax, kDecodeR, H, I, false, M <= 2);
   return c.off;
 }
 
@@ -847,7 +937,7 @@ static int decode_impl(const uint16_t* x, int M, const uint16_t* Wg, const float
   uint32_t* gidx;
   carve_decode(c, M, E, k, Umax, kDecodeR, &logits, &scores, &keys, &inds, &w, &uids, &urows, &ucnt, &uw,
                &gidx, &nu, &status);
-  ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I, false);
+  ExpertsWs ew = carve_experts(c, M, Umax, kDecodeR, H, I, false, M <= 2);
   MIMO_REQUIRE(ws && c.fits(), MIMO_ERR_WORKSPACE, "moe_decode: workspace too small (need %zu)", c.off);
 
   RouterSmallArgs ra{};

@@ -168,6 +168,49 @@ __device__ __forceinline__ void quant_block_fp8_hilo(const float* v, uint32_t* h
   *lsb = (uint8_t)(Y + 127);
 }
 
+// The same split of a 32-value block held by two adjacent lanes (lane pair l, l ^ 1: values 16 (l & 1) .. of the
+// block), 16 bf16 values per lane packed two per word (element 2 j in the low half of p[j]).  Every lane of the
+// wave calls it (the block maxima are exchanged between the pair); per element the operations are those of
+// quant_block_fp8_hilo, so the codes and exponents are the same.  hw, lw: 4 words of codes each; X, Y: the
+// block's hi and lo exponents (E8M0 byte = exponent + 127).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ void quant_pair_fp8_hilo(const uint32_t (&p)[8], uint32_t (&hw)[4], uint32_t (&lw)[4],
+                                                    int* Xo, int* Yo) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(p[j])), fabsf(bf16_hi(p[j]))));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  const int X = fp8_block_exp(amax);
+  const float sx = exp2i(-X), dx = exp2i(X);
+  float ramax = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float v0 = bf16_lo(p[2 * w]), v1 = bf16_hi(p[2 * w]), v2 = bf16_lo(p[2 * w + 1]), v3 = bf16_hi(p[2 * w + 1]);
+    const uint32_t c01 = e4m3_pack2(v0 * sx, v1 * sx);
+    const uint32_t c23 = e4m3_pack2(v2 * sx, v3 * sx);
+    hw[w] = c01 | (c23 << 16);
+    const v2f d01 = e4m3_unpack2(c01), d23 = e4m3_unpack2(c23);
+    ramax = fmaxf(ramax, fabsf(__builtin_fmaf(-d01.x, dx, v0)));
+    ramax = fmaxf(ramax, fabsf(__builtin_fmaf(-d01.y, dx, v1)));
+    ramax = fmaxf(ramax, fabsf(__builtin_fmaf(-d23.x, dx, v2)));
+    ramax = fmaxf(ramax, fabsf(__builtin_fmaf(-d23.y, dx, v3)));
+  }
+  ramax = fmaxf(ramax, __shfl_xor(ramax, 1, 64));
+  const int Y = fp8_block_exp(ramax);
+  const float sy = exp2i(-Y);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float v0 = bf16_lo(p[2 * w]), v1 = bf16_hi(p[2 * w]), v2 = bf16_lo(p[2 * w + 1]), v3 = bf16_hi(p[2 * w + 1]);
+    const v2f d01 = e4m3_unpack2(hw[w] & 0xFFFFu), d23 = e4m3_unpack2(hw[w] >> 16);
+    const float r0 = __builtin_fmaf(-d01.x, dx, v0), r1 = __builtin_fmaf(-d01.y, dx, v1);
+    const float r2 = __builtin_fmaf(-d23.x, dx, v2), r3 = __builtin_fmaf(-d23.y, dx, v3);
+    lw[w] = e4m3_pack2(r0 * sy, r1 * sy) | (e4m3_pack2(r2 * sy, r3 * sy) << 16);
+  }
+  *Xo = X;
+  *Yo = Y;
+}
+
 // ------------------------------------------------------------------ wave reductions (wave64)
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
