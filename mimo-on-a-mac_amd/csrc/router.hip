@@ -142,6 +142,9 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
   const uint16_t* wrow = a.Wg + (size_t)e * a.H + wave * q4;
   uint4 wq[NCH], xq[8][NCH], nw[NCH];
   bool ok[NCH];
+  // the expert's selection bias comes in with the first batch: loaded after the logit stores below it would be
+  // one more memory round trip at the end of every block (the compiler cannot move it above stores it may alias)
+  const float bias_e = a.keys ? a.bias[e] : 0.0f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int off = c * 512 + lane * 8;
@@ -204,7 +207,7 @@ __global__ void __launch_bounds__(256) router_logits_small_kernel(RouterSmallArg
     const float s = sigmoid_spec(l);
     a.logits[r * a.E + e] = l;
     if (a.scores) a.scores[r * a.E + e] = s;
-    if (a.keys) a.keys[r * a.E + e] = s + a.bias[e];
+    if (a.keys) a.keys[r * a.E + e] = s + bias_e;
   }
 }
 
