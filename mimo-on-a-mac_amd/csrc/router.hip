@@ -303,10 +303,28 @@ __global__ void __launch_bounds__(256) router_select_kernel(const float* __restr
   __shared__ float ow[4][16];
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
-  for (int e = lane; e < E; e += 64) {
-    float s = sigmoid_spec(logits[(size_t)t * E + e]);
-    s_row[e] = s;
-    k_row[e] = s + bias[e];
+  if (E <= 256) {   // every logit and bias of the row requested at once, the four sigmoids interleaved
+    float lg[4], bs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j < E ? lane + 64 * j : 0;
+      lg[j] = logits[(size_t)t * E + e];
+      bs[j] = bias[e];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s = sigmoid_spec(lg[j]);
+      if (lane + 64 * j < E) {
+        s_row[lane + 64 * j] = s;
+        k_row[lane + 64 * j] = s + bs[j];
+      }
+    }
+  } else {
+    for (int e = lane; e < E; e += 64) {
+      float s = sigmoid_spec(logits[(size_t)t * E + e]);
+      s_row[e] = s;
+      k_row[e] = s + bias[e];
+    }
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
