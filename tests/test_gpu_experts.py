@@ -187,28 +187,30 @@ def test_workspace_reuse_across_shapes(rng, tiny_pool, mimo_pool):
     assert torch.equal(y1, y2)
 
 
+@pytest.mark.parametrize("M", [1, 2])
 @pytest.mark.parametrize("shape", ["mimo", "tiny"])
-def test_one_row_fast_selection_equals_slot_table_path(rng, shape):
-    """One row with expert ids as slots takes the fast selection (each gate/up block finds its expert from the
-    threshold search alone); an explicit identity slot table takes the general routed path (full selection and
-    grouping in every block).  Both give the same bits, with and without the residual of the layer step, over
-    many rows in a row, and match the oracle."""
+def test_fast_selection_equals_slot_table_path(rng, shape, M):
+    """One or two rows with expert ids as slots take the fast path: each gate/up block finds its expert from the
+    threshold searches alone, blocks cover 16 outputs and write h in bf16, and the down kernel splits h into the
+    hi/lo planes.  An explicit identity slot table takes the general routed path (full selection and grouping in
+    every block, 32-output blocks splitting h themselves).  Both give the same bits, with and without the residual
+    of the layer step, over many steps in a row, and match the oracle."""
     from mimo_stream import MoEBlock, MoELayer, pools
     H, I, E, k = (4096, 2048, 256, 8) if shape == "mimo" else (256, 512, 8, 2)
     bank = pools.random_bank(E, seed=77, hidden=H, inter=I)
     blk, W, bias = _block(rng, bank, H, E, k)
     ref = MoEBlock(blk.router, bank, slot_of=np.arange(E, dtype=np.int32))
-    xs = to_dev_bf16(rand_bf16(rng, (12, H)))
-    for t in range(12):
-        y, inds, w = blk(xs[t:t + 1], return_routes=True)
-        y2, inds2, w2 = ref(xs[t:t + 1], return_routes=True)
+    xs = to_dev_bf16(rand_bf16(rng, (12 * M, H)))
+    for t in range(0, 12 * M, M):
+        y, inds, w = blk(xs[t:t + M], return_routes=True)
+        y2, inds2, w2 = ref(xs[t:t + M], return_routes=True)
         assert torch.equal(inds, inds2) and torch.equal(w, w2)
-        assert torch.equal(y, y2), (shape, t)
+        assert torch.equal(y, y2), (shape, M, t)
     nw = to_dev_bf16(rand_bf16(rng, (H,), 0.2) + 1.0)
     la, lb = MoELayer(blk, nw, 1e-5), MoELayer(ref, nw, 1e-5)
-    for t in range(4):
-        assert torch.equal(la(xs[t:t + 1]), lb(xs[t:t + 1])), (shape, t)
-    if shape == "mimo":           # and against the oracle on the routes the block chose
+    for t in range(0, 4 * M, M):
+        assert torch.equal(la(xs[t:t + M]), lb(xs[t:t + M])), (shape, M, t)
+    if shape == "mimo" and M == 1:           # and against the oracle on the routes the block chose
         pool = pool_np(bank)
         x = bf16_np(xs[:1])
         y, inds, w = blk(xs[:1], return_routes=True)
