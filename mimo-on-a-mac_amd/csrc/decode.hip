@@ -171,9 +171,10 @@ __device__ __forceinline__ void publish_routes(const ExpertsArgs& a, const int32
 }
 
 // FAST2 (routed only; the launcher checks its conditions): two rows with expert ids as slots.
-// HALF (with FAST2): blocks of 256 threads and 16 outputs (wave w: K-range w), four per CU, so that a step's
-// U x I / 16 blocks spread more evenly over the CUs than U x I / 32 larger ones; such a block writes h in bf16
-// and the down kernel splits it (an E8M0 block of h spans 32 outputs, two of these blocks).
+// HALF (the launcher uses it for one or two rows with expert ids as slots, where blocks take the fast selection):
+// blocks of 256 threads and 16 outputs (wave w: K-range w), four per CU, so that a step's U x I / 16 blocks spread
+// more evenly over the CUs than U x I / 32 larger ones; such a block writes h in bf16 and the down kernel splits
+// it (an E8M0 block of h spans 32 outputs, two of these blocks).
 template <int NS, bool ROUTED, bool FAST2, bool HALF = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) decode_gateup_kernel(ExpertsArgs a, int rl) {
   static_assert(!HALF || ROUTED, "16-output blocks only for the routed kernel");
@@ -461,8 +462,8 @@ __host__ __device__ inline DownLds down_lds(int I, int rw, int nroutes) {
 }
 
 // HSPLIT: h comes in bf16 (from the 16-output gate/up blocks) and each wave splits its item's rows into the hi/lo
-// E4M3 planes itself, one 32-block per lane (rows of the K-half at lanes 0-31 and 32-63, so rw <= 2), while its
-// weights stream; the planes and scales are those the gate/up epilogue writes otherwise.
+// E4M3 planes itself while its weights stream, a lane pair per 32-block and the (at most rw <= 2) staged rows one
+// after the other; the planes and scales are those the gate/up epilogue writes otherwise.
 template <int NS, bool HSPLIT = false>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4))) decode_down_combine_kernel(ExpertsArgs a, int rw) {
   extern __shared__ __align__(16) uint8_t dl[];
