@@ -24,6 +24,14 @@
  * read out of bounds, so the outputs of a call whose status is not MIMO_OK are not valid.  The word is
  * written on the stream like every output (read it after the stream's work, no host sync inside the call);
  * NULL keeps it in the workspace.
+ *
+ * Streams: the prefill entry points (mimo_moe_prefill, mimo_moe_prefill_staged, mimo_moe_prefill_block,
+ * mimo_moe_layer_prefill) run part of each grouped GEMM on a side stream forked from and joined back to
+ * `stream` with events; every (device, stream) pair has its own side stream, kept for the life of the
+ * process.  A call therefore orders work only on its own `stream`: prefills on different streams never wait
+ * for each other, and a prefill captured into a HIP graph captures only its own stream's work.  No entry
+ * point builds anything on the device at first use (the sigmoid table is constant data), so the first call
+ * of a process may itself be captured.
  */
 #ifndef MIMO_MOE_H
 #define MIMO_MOE_H

@@ -7,6 +7,7 @@
 #include "device.h"
 #include "host.h"
 #include "router.h"
+#include "sigmoid_table.h"
 
 namespace mimo {
 
@@ -252,12 +253,10 @@ int launch_quantize_fp8_hilo(const uint16_t* x, int64_t rows, int64_t cols, uint
 }
 
 // ------------------------------------------------------------------ bf16 sigmoid table
-static __device__ uint16_t g_sigtab[65536];
-
-__global__ void build_sigtab_kernel(uint16_t* tab) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < 65536) tab[i] = f32_to_bf16(sigmoid_spec(bf16_to_f32((uint16_t)i)));
-}
+// The table is data in the code object (evaluated by the compiler, sigmoid_table.h): nothing is built or
+// synchronised at run time, so any call, including the first prefill of a process under graph capture, only
+// looks up its device address (no stream work).
+static __device__ sigtab_gen::Table g_sigtab = sigtab_gen::make();
 
 static std::mutex g_sig_mu;
 static const uint16_t* g_sig_ptr[64];
@@ -274,12 +273,6 @@ const uint16_t* sigtab_device(int* err) {
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_sigtab));
     if (e != hipSuccess) {
       *err = set_error(MIMO_ERR_HIP, "hipGetSymbolAddress(sigtab): %s", hipGetErrorString(e));
-      return nullptr;
-    }
-    build_sigtab_kernel<<<256, 256, 0, 0>>>(static_cast<uint16_t*>(p));
-    e = hipDeviceSynchronize();     // once per device and process, before any use
-    if (e != hipSuccess) {
-      *err = set_error(MIMO_ERR_HIP, "building the sigmoid table: %s", hipGetErrorString(e));
       return nullptr;
     }
     g_sig_ptr[dev] = static_cast<const uint16_t*>(p);

@@ -70,14 +70,18 @@ __device__ __forceinline__ float exp2i(int X) {   // 2^X for -127 <= X <= 127, e
 // Signed E4M3 code of v / 2^X (positive zero for a zero magnitude); writes the residual v - code * 2^X, computed
 // as one fused multiply-add: the difference is exact and the product, which can pass the fp32 range for the
 // largest blocks (448 * 2^120), is never rounded on its own.
+// A non-finite v (NaN or +-inf; E4M3 has no infinity) gets the E4M3 NaN code 0x7F and a NaN residual, as the
+// hardware conversion gives, so every product of its row is NaN.
 __device__ __forceinline__ uint32_t e4m3_encode(float v, int X, float* res) {
   float inv = exp2i(-X);        // exact when -X in range; X >= -127 so -X <= 127
   float y = fabsf(v) * inv;
   uint32_t mag = e4m3_mag_code(y);
   float dm = e4m3_decode_mag(mag);
   uint32_t sgn = (mag != 0u && v < 0.0f) ? 0x80u : 0u;
-  *res = __builtin_fmaf(sgn ? dm : -dm, exp2i(X), v);
-  return mag | sgn;
+  const bool finite = fabsf(v) <= 3.40282347e38f;
+  const float r = __builtin_fmaf(sgn ? dm : -dm, exp2i(X), v);
+  *res = finite ? r : __uint_as_float(0x7FC00000u);
+  return finite ? (mag | sgn) : 0x7Fu;
 }
 
 // Two E4M3 codes (bits 0-7 and 8-15) of values already divided by their block scale (|y| <= 448) from the

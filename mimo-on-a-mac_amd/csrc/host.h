@@ -45,7 +45,7 @@ struct ProfScope {
   ~ProfScope() { prof_end(st); }
 };
 
-// Device address of the bf16 sigmoid table (built on first use on the current device).
+// Device address of the bf16 sigmoid table on the current device (compile-time data; no stream work).
 const uint16_t* sigtab_device(int* err);
 
 // Bump allocator over a caller workspace.

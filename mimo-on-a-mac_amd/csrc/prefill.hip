@@ -15,10 +15,12 @@
 // four 16-row weight tiles, the hi and lo planes accumulating into the same tile.  The epilogue stages results in
 // LDS and writes 16-byte pieces.
 #include <atomic>
+#include <memory>
 #include <mutex>
 
 #include "device.h"
 #include "host.h"
+#include "keyed_once.h"
 #include "layer.h"
 #include "router.h"
 
@@ -542,33 +544,33 @@ static PrefillWs carve_prefill(Carve& c, int T, int k, int S, int H, int I, int 
 }
 
 // stage (optional): a second bank whose slots follow the bank's (slot ids bank->n_slots ...)
-// The narrow tiles of a GEMM run on a side stream of the device (default priority, created with two events on
-// the device's first prefill call) concurrently with the wide tiles on the caller's stream: the narrow launch
-// waits for the work queued on the caller's stream, and the caller's stream waits for the narrow launch before
-// its next work.  The fork and join of one call are enqueued under a lock, so calls from several host threads
-// never wait on each other's events; their narrow launches queue one after another on the side stream.
+// The narrow tiles of a GEMM run on a side stream concurrently with the wide tiles on the caller's stream: the
+// narrow launch waits for the work queued on the caller's stream, and the caller's stream waits for the narrow
+// launch before its next work.  Each (device, caller stream) pair has a side stream of its own (default priority,
+// created with its two events on the pair's first prefill and kept for the life of the process), so a prefill
+// waits only for work of its own caller stream: calls on different streams create no ordering between those
+// streams, and a capture on one stream never joins another stream's work.  The fork and join of one call are
+// enqueued under the pair's lock, so host threads sharing a caller stream never wait on each other's events.
 struct SideStream {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
   std::mutex mu;
 };
-static SideStream* side_stream() {
-  static std::mutex mu;
-  static SideStream per[64];
+static SideStream* side_stream(hipStream_t caller) {
+  static KeyedOnce<std::pair<int, hipStream_t>, SideStream> per;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> g(mu);
-  SideStream& ss = per[dev];
-  if (!ss.s) {
-    if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) {
-      (void)hipStreamDestroy(ss.s);
-      ss.s = nullptr;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  return per.get(std::make_pair(dev, caller), []() -> std::unique_ptr<SideStream> {
+    std::unique_ptr<SideStream> ss(new SideStream);
+    if (hipStreamCreateWithFlags(&ss->s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&ss->fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ss->join, hipEventDisableTiming) != hipSuccess) {
+      if (ss->fork) (void)hipEventDestroy(ss->fork);
+      (void)hipStreamDestroy(ss->s);
       return nullptr;
     }
-  }
-  return &ss;
+    return ss;
+  });
 }
 
 template <bool GATEUP, bool WIDE> static int pf_allow_lds() {
@@ -624,7 +626,7 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   auto grid_of = [&](int cap, int obn) { return 8 * (int)(((int64_t)cap * obn + 7) / 8); };
   using NS = PfShape<false>;
   using WS = PfShape<true>;
-  SideStream* ss = tl.scap ? side_stream() : nullptr;
+  SideStream* ss = tl.scap ? side_stream(st) : nullptr;
   if (tl.scap && !ss) return set_error(MIMO_ERR_HIP, "moe prefill: cannot create the side stream");
   // one GEMM: narrow tiles on the side stream, wide tiles on st, joined before st's next work
   auto gemm = [&](auto narrow_kernel, auto wide_kernel, int obn_narrow, int obn_wide) -> int {

@@ -1,5 +1,7 @@
 """Shared helpers for the GPU parity tests: device tensors <-> oracle numpy arrays."""
 import os
+import subprocess
+import sys
 
 import numpy as np
 import torch
@@ -76,3 +78,41 @@ def shared_routes(rng, M, S, k):
         else:
             rows.append(rng.choice(S, k, replace=False))
     return np.stack(rows).astype(np.int32)
+
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# Preamble of child-process GPU checks: inputs made by torch alone (no library call), a bank of random E2M1
+# codes (every code) with E8M0 scales 118..122.
+CHILD_COMMON = r"""
+import sys, numpy as np, torch
+from mimo_stream import _lib, pools
+torch.manual_seed(5)
+dev = torch.device("cuda")
+
+def torch_bank(E, H, I):
+    # random E2M1 codes (every code) and E8M0 scales 118..122, made by torch only
+    bank = {}
+    for k, (o, i) in pools.shapes(H, I).items():
+        bank[f"{k}_w"] = torch.randint(-2**31, 2**31 - 1, (E, o, i // 8), dtype=torch.int32, device=dev)
+        bank[f"{k}_s"] = torch.randint(118, 123, (E, o, i // 32), dtype=torch.uint8, device=dev)
+    return bank
+
+def bf16(*shape, scale=1.0):
+    return (torch.randn(*shape, device=dev) * scale).to(torch.bfloat16)
+
+def say(msg):
+    print(msg, flush=True)
+"""
+
+
+def run_child(code, marker, timeout=300):
+    """Run a Python GPU check in a fresh process (library and package importable); it must exit 0 and print
+    marker."""
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([ROOT, os.path.join(ROOT, "mimo-on-a-mac_amd"), env.get("PYTHONPATH", "")])
+    p = subprocess.run([sys.executable, "-u", "-c", code], env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True, timeout=timeout)
+    assert p.returncode == 0 and marker in p.stdout, f"child exited {p.returncode}:\n{p.stdout[-3000:]}"
+
+

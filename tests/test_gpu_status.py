@@ -53,7 +53,10 @@ def _ws(name, *size_args):
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_decode_status(parts, M):
-    """M = 1, 2, 4 select inside the gate/up kernel, M = 8 (32 routes) in the separate selection launch."""
+    """With 16 experts and top-4 every batch here has at most 16 distinct experts (Umax = min(M k, E) <= 16), so
+    the gate/up kernel's blocks select and group the routes themselves at every M (the one-row and two-row fast
+    paths when no slot table is given); test_decode_status_selection_launch covers the separate selection
+    launch."""
     bank, W, bias, x, _ = parts
     b = pools.bank_struct(bank)
     y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
@@ -68,6 +71,36 @@ def test_decode_status(parts, M):
         _lib.call("mimo_moe_decode", _lib.ptr(x[:M]), M, _lib.ptr(W), _lib.ptr(bias), None, E, K, b, _lib.ptr(y),
                   None, None, _lib.ptr(st), _lib.ptr(ws), nb, _lib.stream_ptr())
     assert _status(run_none) == _lib.MIMO_OK
+
+
+@pytest.mark.parametrize("M", [3, 8])
+def test_decode_status_selection_launch(M):
+    """Batches with more than 16 possible distinct experts (64 experts, top-8: Umax = min(M k, E) = 24 or 64)
+    select and group their routes in the separate selection launch, which writes the status word there: OK,
+    a selected expert missing from the slot table, and one mapped past the bank."""
+    E2, K2 = 64, 8
+    bank = pools.random_bank(E2, seed=37, hidden=H, inter=I)
+    b = pools.bank_struct(bank)
+    g = torch.Generator().manual_seed(37)
+    W = (torch.randn(E2, H, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    bias = torch.zeros(E2)
+    bias[FORCED] = 10.0
+    bias = bias.cuda()
+    x = torch.randn(M, H, generator=g).to(torch.bfloat16).cuda()
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    ws, nb = _ws("mimo_moe_decode_workspace_size", M, E2, K2, H, I)
+    ident = torch.arange(E2, dtype=torch.int32)
+    missing, beyond = ident.clone(), ident.clone()
+    missing[FORCED] = -1
+    beyond[FORCED] = E2
+    for name, tab, want in (("identity", ident, _lib.MIMO_OK), ("missing", missing, _lib.ERR_SLOT),
+                            ("beyond", beyond, _lib.ERR_SLOT)):
+        tab = tab.cuda()
+
+        def run(st):
+            _lib.call("mimo_moe_decode", _lib.ptr(x), M, _lib.ptr(W), _lib.ptr(bias), _lib.ptr(tab), E2, K2, b,
+                      _lib.ptr(y), None, None, _lib.ptr(st), _lib.ptr(ws), nb, _lib.stream_ptr())
+        assert _status(run) == want, (name, M)
 
 
 @pytest.mark.parametrize("M", [1, 4])

@@ -1,12 +1,14 @@
 """mimo_moe_layer_decode_noalloc (the layer decode step with the library's own per-GPU scratch instead of a caller
 workspace) gives the bits of mimo_moe_layer_decode with a workspace: h, r, the routes and the status, on calls in
 a row whose batches shrink (the scratch keeps the previous call's contents), at the MiMo layer shape and the tiny
-one, with a slot table that leaves an expert out (status reported)."""
+one, with a slot table that leaves an expert out (status reported); and the step under HIP graph capture at 1, 2
+and 8 rows, as the first library call of a fresh process (its scratch address lookup and LDS attribute happen on
+that call) and after eager warm-up calls, every replay equal to the eager results bit for bit."""
 import numpy as np
 import pytest
 import torch
 
-from helpers import rand_bf16, to_dev_bf16
+from helpers import CHILD_COMMON, rand_bf16, run_child, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -62,3 +64,101 @@ def test_noalloc_matches_workspace_entry_point(rng, shape):
     assert got[4] == ref[4] != 0
     for a, c in zip(got[:4], ref[:4]):
         assert torch.equal(a, c)
+
+
+# The first no-allocation call of a process (scratch address lookup and LDS attribute on that call) under capture.
+NOALLOC_CHILD = CHILD_COMMON + r"""
+H, I, E, k = 4096, 2048, 256, 8
+bank = torch_bank(E, H, I)
+b = pools.bank_struct(bank)
+W = bf16(E, H, scale=0.02)
+bias = torch.randn(E, device=dev) * 1e-3
+nw = (1.0 + 0.1 * torch.randn(H, device=dev)).to(torch.bfloat16)
+xs = bf16(8, H)
+ROWS = (1, 2, 8)
+def outs(M):
+    return (torch.empty(M, H, dtype=torch.bfloat16, device=dev), torch.empty(M, H, dtype=torch.bfloat16, device=dev),
+            torch.empty(M, k, dtype=torch.int32, device=dev), torch.empty(M, k, dtype=torch.float32, device=dev),
+            torch.full((1,), 77, dtype=torch.int32, device=dev))
+def step(noalloc, M, o, ws=None):
+    head = (_lib.ptr(xs[:M]), M, _lib.ptr(nw), 1e-6, _lib.ptr(W), _lib.ptr(bias), None, E, k, b,
+            *[_lib.ptr(t) for t in o])
+    if noalloc:
+        _lib.call("mimo_moe_layer_decode_noalloc", *head, _lib.stream_ptr())
+    else:
+        _lib.call("mimo_moe_layer_decode", *head, _lib.ptr(ws), ws.numel(), _lib.stream_ptr())
+got = {M: outs(M) for M in ROWS}
+ref = {M: outs(M) for M in ROWS}
+wss = {M: torch.empty(_lib.load().mimo_moe_layer_decode_workspace_size(M, E, k, H, I), dtype=torch.uint8, device=dev)
+       for M in ROWS}
+torch.cuda.synchronize()
+say("capturing the first no-allocation decode steps of the process")
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    for M in ROWS:
+        step(True, M, got[M])
+say("captured; eager reference")
+for M in ROWS:
+    step(False, M, ref[M], wss[M])
+torch.cuda.synchronize()
+for rep in range(3):
+    for M in ROWS:
+        for t in got[M]:
+            t.fill_(3)
+    g.replay()
+    torch.cuda.synchronize()
+    for M in ROWS:
+        for name, a, c in zip(("h", "r", "inds", "w", "status"), got[M], ref[M]):
+            assert torch.equal(a, c), f"replay {rep}, {M} rows: {name} differs"
+        assert int(got[M][4].item()) == 0
+    step(True, 8, outs(8))                   # eager no-allocation and workspace calls between replays
+    step(False, 2, outs(2), wss[2])
+    torch.cuda.synchronize()
+    say(f"replay {rep} ok")
+say("NOALLOC_FIRST_CALL_OK")
+"""
+
+
+def test_first_noalloc_decode_of_a_process_captured():
+    run_child(NOALLOC_CHILD, "NOALLOC_FIRST_CALL_OK")
+
+
+def test_noalloc_decode_captured_after_warmup(rng):
+    from mimo_stream import _lib, pools
+    H, I, E, k = 4096, 2048, 256, 8
+    bank = pools.random_bank(E, seed=91, hidden=H, inter=I)
+    b = pools.bank_struct(bank)
+    W = to_dev_bf16(rand_bf16(rng, (E, H), 0.02))
+    bias = torch.from_numpy((rng.standard_normal(E) * 1e-3).astype(np.float32)).cuda()
+    nw = to_dev_bf16(rand_bf16(rng, (H,), 0.1) + 1.0)
+    xs = to_dev_bf16(rand_bf16(rng, (8, H)))
+    rows = (1, 2, 8)
+
+    def outs(M):
+        return (torch.empty(M, H, dtype=torch.bfloat16, device="cuda"),
+                torch.empty(M, H, dtype=torch.bfloat16, device="cuda"),
+                torch.empty(M, k, dtype=torch.int32, device="cuda"),
+                torch.empty(M, k, dtype=torch.float32, device="cuda"),
+                torch.full((1,), 77, dtype=torch.int32, device="cuda"))
+
+    def step(M, o):
+        _lib.call("mimo_moe_layer_decode_noalloc", _lib.ptr(xs[:M]), M, _lib.ptr(nw), 1e-6, _lib.ptr(W),
+                  _lib.ptr(bias), None, E, k, b, *[_lib.ptr(t) for t in o], _lib.stream_ptr())
+
+    ref = {M: outs(M) for M in rows}
+    for M in rows:                       # warm-up: these are also the eager references
+        step(M, ref[M])
+    got = {M: outs(M) for M in rows}
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for M in rows:
+            step(M, got[M])
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for M in rows:
+            for name, a, c in zip(("h", "r", "inds", "w", "status"), got[M], ref[M]):
+                assert torch.equal(a, c), (rep, M, name)
+        step(8, outs(8))                 # eager calls on the same scratch between replays
+        torch.cuda.synchronize()
