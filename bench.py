@@ -211,6 +211,34 @@ def zipf_routes(T, seed, nin):
     return out
 
 
+def profile_counts():
+    """Measured per-layer expert popularity of MiMo-V2.6-Flash (tests/golden/expert_profile.npz, the reference's
+    engine/mimo_stream/data/expert_profile.npz): int64 [47, 256] selection counts, row i = MoE layer i + 1."""
+    import numpy as np
+    with np.load(os.path.join(ROOT, "tests", "golden", "expert_profile.npz"), allow_pickle=False) as z:
+        return z["counts"]
+
+
+def profile_routes(T, seed, layer_rows):
+    """One routing of T tokens per entry of layer_rows: top-8 distinct experts per token drawn with that layer's
+    measured popularity (Gumbel top-k on log(count), experts never selected in the profile excluded), and
+    normalised random weights."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    counts = profile_counts()
+    out = []
+    for l in layer_rows:
+        c = counts[l].astype(np.float64)
+        with np.errstate(divide="ignore"):
+            logp = np.log(c / c.sum())
+        g = rng.gumbel(size=(T, E)) + logp[None, :]
+        inds = np.argsort(-g, axis=1)[:, :K].astype(np.int32)
+        w = rng.random((T, K)).astype(np.float32)
+        w /= w.sum(1, keepdims=True)
+        out.append((inds, w))
+    return out
+
+
 def hot_routes(T, seed, nin, n_hot=PF_HOT_EXPERTS):
     """`nin` routings of T tokens concentrated on `n_hot` experts (a seeded subset): each token takes 8 of them
     uniformly at random, so every expert gets about T * 8 / n_hot routes and every row tile is a full wide tile
@@ -277,20 +305,26 @@ def hot_prefill_case(layers, T, device):
     return r
 
 
-def stack_case(layers, M, tokens, device, seed):
+def stack_case(layers, M, tokens, device, seed, popularity="zipf"):
     """One decode step through every resident layer (48 = the MiMo stack): per-layer steered hidden states
-    with Zipf(1.1) expert popularity; reports MoE time per token and aggregate GB/s."""
+    whose experts follow Zipf(1.1) popularity, or (popularity="profile") the measured popularity of the matching
+    MiMo layer (layer l uses profile row l mod 47); reports MoE time per token and aggregate GB/s."""
     import numpy as np
     import torch
     rng = np.random.default_rng(seed)
     n = len(layers.blocks)
     p = 1.0 / np.arange(1, E + 1) ** 1.1
     p /= p.sum()
+    counts = profile_counts() if popularity == "profile" else None
     Xd, Us = [], []
     for t in range(tokens):
         for l in range(n):
-            perm = np.random.default_rng(10 * l + 1).permutation(E)
-            sets = [list(perm[rng.choice(E, K, replace=False, p=p)]) for _ in range(M)]
+            if counts is not None:
+                pl = counts[l % len(counts)] / counts[l % len(counts)].sum()
+                sets = [list(rng.choice(E, K, replace=False, p=pl)) for _ in range(M)]
+            else:
+                perm = np.random.default_rng(10 * l + 1).permutation(E)
+                sets = [list(perm[rng.choice(E, K, replace=False, p=p)]) for _ in range(M)]
             Xd.append(torch.from_numpy(steered_rows(rng, layers.W[l], sets)).to(torch.bfloat16).to(device))
             Us.append(len(np.unique(np.concatenate(sets))))
     blocks = layers.blocks
@@ -718,15 +752,19 @@ def main():
                 log(f"[bench] decode M={M}: {r['ms_per_layer'] * 1e3:.1f} us/layer, U={r['distinct_experts']:.1f}, {r['GBps']:.0f} GB/s")
             except Exception as e:    # an extra measurement never hides the headline
                 extra[f"decode_m{M}"] = {"error": repr(e)}
-        for T in (512, 2048):
+        for T, pop in ((512, "zipf"), (2048, "zipf"), (2048, "profile")):
+            key = f"prefill_t{T}" + ("_profile" if pop == "profile" else "")
             try:
-                r = prefill_case(layers, T, 20, 3, seed=20 + T, device=device)
+                routes = profile_routes(T, 20 + T, (0, 14, 29, 43)) if pop == "profile" else None
+                r = prefill_case(layers, T, 20, 3, seed=20 + T, device=device, routes=routes)
                 kt2 = kernel_times(r.pop("_fn"), 4)
                 r["kernel_us"] = {k: round(v[0] * 1e3, 1) for k, v in kt2.items()}
-                extra[f"prefill_t{T}"] = r
-                log(f"[bench] prefill T={T}: {r['ms_per_layer']:.3f} ms/layer, {r['tokens_per_s']:.0f} tok/s")
+                if pop == "profile":
+                    r["routing"] = "measured MiMo popularity, profile layers 1, 15, 30, 44"
+                extra[key] = r
+                log(f"[bench] prefill T={T} ({pop}): {r['ms_per_layer']:.3f} ms/layer, {r['tokens_per_s']:.0f} tok/s")
             except Exception as e:
-                extra[f"prefill_t{T}"] = {"error": repr(e)}
+                extra[key] = {"error": repr(e)}
         key = f"prefill_t2048_hot{PF_HOT_EXPERTS}"
         try:
             extra[key] = hot_prefill_case(layers, 2048, device)
@@ -734,13 +772,14 @@ def main():
                 f"gate/up {extra[key]['gateup']['useful_TFLOPs']:.0f} useful TFLOP/s")
         except Exception as e:
             extra[key] = {"error": repr(e)}
-        for M in (1, 4):
+        for M, pop in ((1, "zipf"), (4, "zipf"), (1, "profile"), (4, "profile")):
+            key = f"stack{args.layers}_m{M}" + ("_profile" if pop == "profile" else "")
             try:
-                r = stack_case(layers, M, tokens=4, device=device, seed=30 + M)
-                extra[f"stack{args.layers}_m{M}"] = r
-                log(f"[bench] stack M={M}: {r['ms_per_token']:.3f} ms/token, {r['GBps']:.0f} GB/s")
+                r = stack_case(layers, M, tokens=4, device=device, seed=30 + M, popularity=pop)
+                extra[key] = r
+                log(f"[bench] stack M={M} ({pop}): {r['ms_per_token']:.3f} ms/token, {r['GBps']:.0f} GB/s")
             except Exception as e:
-                extra[f"stack{args.layers}_m{M}"] = {"error": repr(e)}
+                extra[key] = {"error": repr(e)}
         for T, st in ((1, min(args.steps, 300)), (2048, 10)):
             try:
                 r = layer_case(layers, T, st, 3, seed=40 + T, device=device)

@@ -131,11 +131,21 @@ def pair_outputs(x, pool, tok, slot):
     slot = np.asarray(slot)
     H = pool.p["down_w"].shape[1]
     out = np.zeros((len(tok), H), np.float32)
-    for s in np.unique(slot):
+
+    def one(s):      # every slot's pairs are independent: slots run on a thread pool (numpy releases the GIL)
         sel = np.nonzero(slot == s)[0]
         xr = x[tok[sel]]
         h = swiglu_bf16(pool.dot("gate", s, xr), pool.dot("up", s, xr))
         out[sel] = mxfp4.round_bf16(pool.dot("down", s, h))
+
+    slots = np.unique(slot)
+    if len(slots) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(min(8, len(slots))) as ex:
+            list(ex.map(one, slots))
+    else:
+        for s in slots:
+            one(s)
     return out
 
 

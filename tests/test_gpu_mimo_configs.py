@@ -14,7 +14,10 @@ hidden 256, intermediate 512):
             popularity ranks (the most popular one, cut into many 64-route tiles, down
             to experts with a single route), so the oracle needs only Q's weights while every tile of those
             experts, both tile shapes and multi-term combines are checked; tokens with no route into Q must come
-            out exactly zero.  A second call with every weight nonzero is compared on 4 random tokens.
+            out exactly zero.  A second call with every weight nonzero is compared on 64 sampled tokens (16 at the
+            three larger chunks); routes and samples come from a per-run seed.
+  profile   2048 tokens routed with the measured per-layer popularity of MiMo layers 1 and 44
+            (tests/golden/expert_profile.npz, from the reference's engine/mimo_stream/data/expert_profile.npz).
   stack     48 layers (164 GB of experts resident), one decode step through every layer at 1 and 4 rows: layers
             0, 23 and 47 against the oracle, every layer bit-identical on a rerun.
 
@@ -175,15 +178,21 @@ def _q_experts(counts):
     return np.unique(np.array(q, np.int64))
 
 
-@pytest.mark.parametrize("T", [512, 2048, 4096, 5001, 6250])
-def test_prefill_zipf_every_token(rng, stack, T):
-    """Every token of a Zipf-routed chunk against the oracle (weights on the routes to a set of experts spread
-    over the popularity ranks).  4096 tokens are the reference engine's prefill chunk (32,768 sorted routes);
-    5001 and 6250 tokens give 40,008 and 50,000 sorted routes, past 32,767 and not multiples of 64, the row
-    counts the reference checks its sorted grouped GEMM at (bench/scripts/gather_qmm_sorted_check.py:36)."""
-    blk = stack[2]
+def _profile_routes(rng, T, profile_row):
+    """Per-token top-8 without replacement from a measured MiMo layer popularity (tests/golden/expert_profile.npz,
+    the reference's engine/mimo_stream/data/expert_profile.npz), Gumbel top-k on log(count)."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import make_expert_profile as mep
+    c = mep.load()[1][profile_row].astype(np.float64)
+    with np.errstate(divide="ignore"):
+        logp = np.log(c / c.sum())
+    g = rng.gumbel(size=(T, E)) + logp[None, :]
+    return np.argsort(-g, axis=1)[:, :K].astype(np.int32)
+
+
+def _prefill_every_token(rng, blk, T, inds, tag, n_full):
     x = rand_bf16(rng, (T, H))
-    inds = zipf_routes(rng, T, E, K)
     counts = np.bincount(inds.reshape(-1), minlength=E)
     Q = _q_experts(counts)
     inQ = np.isin(inds, Q)
@@ -203,17 +212,50 @@ def test_prefill_zipf_every_token(rng, stack, T):
     Y[tok, j] = Yq
     oy = ox.weighted_sum_bf16(Y, wq)
     top = int(Q[np.argmax(counts[Q])])
-    _record(f"prefill {T} tokens, routes to {Q.size} experts", yn, oy, tokens=T, q_experts=int(Q.size),
+    _record(f"prefill {T} tokens{tag}, routes to {Q.size} experts", yn, oy, tokens=T, q_experts=int(Q.size),
             q_routes=int(inQ.sum()), tokens_compared=int(T), top_expert_routes=int(counts[top]),
             top_expert_wide_tiles=int(-(-counts[top] // 64)), experts_touched=int((counts > 0).sum()))
-    # every weight nonzero: the full k-term combine of 4 random tokens
+    # every weight nonzero: the full k-term combine (every route's expert output) of n_full random tokens
     wf = (w / w.sum(1, keepdims=True)).astype(np.float32)
     yf = bf16_np(blk._moe_prefill(xd, idd, torch.from_numpy(wf).cuda()))
-    sample = rng.choice(T, 4, replace=False)
+    sample = np.sort(rng.choice(T, n_full, replace=False))
     pool, remap = _subpool(blk.bank, inds[sample])
-    oyf = np.stack([ox.gather_m1(x[t], pool, remap[inds[t]], wf[t]) for t in sample])
-    _record(f"prefill {T} tokens, all weights, 4 tokens", yf[sample], oyf,
-            ox.reference_fp32(x[sample], pool, remap[inds[sample]], wf[sample]), tokens=T)
+    tok = np.repeat(np.arange(n_full), K)
+    Ys = ox.pair_outputs(x[sample], pool, tok, remap[inds[sample]].reshape(-1)).reshape(n_full, K, H)
+    oyf = ox.weighted_sum_bf16(Ys, wf[sample])
+    _record(f"prefill {T} tokens{tag}, all weights, {n_full} tokens", yf[sample], oyf,
+            ox.reference_fp32(x[sample], pool, remap[inds[sample]], wf[sample]), tokens=T,
+            experts_compared=int(len(np.unique(inds[sample]))))
+
+
+def _run_seed():
+    """A fresh seed per run for the sampled checks (printed, so a failing run can be repeated with
+    MIMO_TEST_SEED)."""
+    seed = int(os.environ.get("MIMO_TEST_SEED", np.random.SeedSequence().entropy % (1 << 31)))
+    print(f"[seed] MIMO_TEST_SEED={seed}", flush=True)
+    return seed
+
+
+@pytest.mark.parametrize("T", [512, 2048, 4096, 5001, 6250])
+def test_prefill_zipf_every_token(stack, T):
+    """Every token of a Zipf-routed chunk against the oracle (weights on the routes to a set of experts spread
+    over the popularity ranks), and the full combine of sampled tokens with every weight nonzero (64 tokens at
+    512 and 2048, 16 at the larger chunks).  4096 tokens are the reference engine's prefill chunk (32,768 sorted
+    routes); 5001 and 6250 tokens give 40,008 and 50,000 sorted routes, past 32,767 and not multiples of 64, the
+    row counts the reference checks its sorted grouped GEMM at (bench/scripts/gather_qmm_sorted_check.py:36).
+    Routes, activations and samples come from a per-run seed."""
+    rng = np.random.default_rng(_run_seed() + T)
+    inds = zipf_routes(rng, T, E, K)
+    _prefill_every_token(rng, stack[2], T, inds, "", 64 if T <= 2048 else 16)
+
+
+@pytest.mark.parametrize("profile_row", [0, 43])
+def test_prefill_measured_popularity_every_token(stack, profile_row):
+    """2048 tokens routed with the measured popularity of MiMo layers 1 and 44 (the reference's expert profile):
+    the prefill tiling's mix of wide and narrow tiles under real routing, every token and 64 full combines."""
+    rng = np.random.default_rng(_run_seed() + 7 * profile_row)
+    inds = _profile_routes(rng, 2048, profile_row)
+    _prefill_every_token(rng, stack[3], 2048, inds, f" (MiMo layer {profile_row + 1} popularity)", 64)
 
 
 @pytest.mark.parametrize("M", [1, 4])
