@@ -306,9 +306,11 @@ __device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;
 }
+// The LDS byte offset of a pointer into LDS: the low 32 bits of its generic address (the LDS aperture puts the
+// offset there).  No address-space cast: its null check, folded against the aperture base in divergent code,
+// made the gfx950 backend emit an invalid compare.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
 // The base address operands of these copies are SGPRs that are often written by v_readfirstlane just before
 // the asm; a VMEM instruction reading an SGPR that a VALU instruction wrote needs 5 wait states, which the
