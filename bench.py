@@ -411,7 +411,9 @@ def cpu_baseline(layers, seconds, n_layers=2):
     """The one-row MoE-layer decode (Router + _gather_m1, model.py:58-65, :173-182) on the host CPU: the fp32
     PyTorch restatement oracle.cpu_decode on every thread PyTorch is given (OMP_NUM_THREADS), over host copies
     of `n_layers` whole resident layers (3.42 GB each, so the experts come from DRAM, not cache), for about
-    `seconds`; returns GB/s with the same byte accounting as the GPU figure."""
+    `seconds` split between its two forms of the expert products: per-32-group sums times the group scale
+    (group_dot, no fp32 weight matrix; the reported value) and the whole-matrix dequantise-then-multiply port.
+    Returns GB/s with the same byte accounting as the GPU figure."""
     import numpy as np
     import torch
     from oracle import cpu_decode as cd, mxfp4 as oq
@@ -422,20 +424,28 @@ def cpu_baseline(layers, seconds, n_layers=2):
         b = layers.blocks[l]
         host.append(({k: v.cpu() for k, v in b.bank.items()}, torch.from_numpy(layers.W[l]),
                      b.router.e_score_correction_bias.cpu()))
-    done, t_cpu, nbytes = 0, 0.0, 0.0
-    cd.decode_step(torch.zeros(H), host[0][1], host[0][2], host[0][0])             # warm-up, not timed
-    while t_cpu < seconds and done < 200:
-        pools, W, bias = host[done % len(host)]
-        x = torch.from_numpy(oq.round_bf16(steered_rows(rng, W.numpy(), controlled_sets(rng, 1)))[0])
-        t0 = time.perf_counter()
-        _, inds, _ = cd.decode_step(x, W, bias, pools, K)
-        t_cpu += time.perf_counter() - t0
-        done += 1
-        nbytes += len(np.unique(inds.numpy())) * 13369344 + ROUTER_BYTES + 2 * H * 2
-    return {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{done} one-row MoE-layer decode steps (router + 8 MXFP4 experts + combine) over host copies "
-                      f"of {len(host)} of the same layers, fp32 PyTorch restatement (oracle/cpu_decode.py), "
-                      f"{threads} threads, {t_cpu:.1f} s; host: {os.cpu_count()} logical CPUs ({_cpu_model()})"}
+    res = {}
+    for grouped, budget in ((True, 0.6 * seconds), (False, 0.4 * seconds)):
+        cd.decode_step(torch.zeros(H), host[0][1], host[0][2], host[0][0], K, grouped)   # warm-up, not timed
+        done, t_cpu, nbytes = 0, 0.0, 0.0
+        while t_cpu < budget and done < 200:
+            pools, W, bias = host[done % len(host)]
+            x = torch.from_numpy(oq.round_bf16(steered_rows(rng, W.numpy(), controlled_sets(rng, 1)))[0])
+            t0 = time.perf_counter()
+            _, inds, _ = cd.decode_step(x, W, bias, pools, K, grouped)
+            t_cpu += time.perf_counter() - t0
+            done += 1
+            nbytes += len(np.unique(inds.numpy())) * 13369344 + ROUTER_BYTES + 2 * H * 2
+        res[grouped] = (nbytes / t_cpu / 1e9, done, t_cpu)
+    (g_val, g_n, g_t), (p_val, p_n, p_t) = res[True], res[False]
+    return {"value": g_val, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{g_n} one-row MoE-layer decode steps (router + 8 MXFP4 experts + combine) over host copies "
+                      f"of {len(host)} of the same layers, fp32 PyTorch restatement (oracle/cpu_decode.py, "
+                      f"per-32-group sums times the group scale), {threads} threads, {g_t:.1f} s; host: "
+                      f"{os.cpu_count()} logical CPUs ({_cpu_model()})",
+            "dequant_matrix_port": {"value": p_val, "unit": "GB/s", "steps": p_n, "seconds": round(p_t, 2),
+                                    "is": "the same steps with each expert matrix dequantised to fp32, then "
+                                          "multiplied"}}
 
 
 def _cpu_model():

@@ -10,7 +10,12 @@ it rather than as a pin:
     one E8M0 scale per 32, kernels.py:5-30), a = bf16(gate . x), b = bf16(up . x), h = bf16(bf16(a * sig(a)) * b)
     with sig the bf16 sigmoid table (kernels.py:79-82, :138-146), y_e = bf16(down . h), y = bf16(sum_j y_e_j * w_j).
 Dot products accumulate in fp32 in PyTorch's order and torch.sigmoid gives the sigmoid, so results agree with the
-oracle within the same bf16 tolerance as the GPU path (tests/test_oracle_cpu_decode.py)."""
+oracle within the same bf16 tolerance as the GPU path (tests/test_oracle_cpu_decode.py).
+
+Two ways to form each expert's matrix-vector products are kept: `gather_m1` dequantises the whole weight matrix
+to fp32 and multiplies (the plain port), `gather_m1_grouped` never forms it: per block of rows it sums the
+unscaled E2M1 values times x within each 32-element group and then multiplies the group sums by the group's
+E8M0 scale (the order a CPU kernel for the format would use)."""
 import torch
 
 from .mxfp4 import E2M1_VALUES
@@ -57,7 +62,37 @@ def gather_m1(x, pools, inds, w):
     return _bf16(acc)
 
 
-def decode_step(x, W, bias, pools, k=8):
+def group_dot(q, s, x, rows=128):
+    """q int32 [out, in/8], s uint8 [out, in/32], x fp32 [in] -> fp32 [out]: y[o] = sum over groups g of
+    2^(s[o, g] - 127) * sum_j e2m1(q[o, 32 g + j]) * x[32 g + j] (scale 255: NaN), `rows` rows at a time, so no
+    fp32 copy of the matrix is formed (only the unscaled values of one block of rows)."""
+    out_dim, G = s.shape
+    xg = x.reshape(G, 16, 2)
+    sc = torch.ldexp(torch.ones((), dtype=torch.float32), s.to(torch.int32) - 127)
+    sc = torch.where(s == 255, torch.full_like(sc, float("nan")), sc)
+    y = torch.empty(out_dim, dtype=torch.float32)
+    for r0 in range(0, out_dim, rows):
+        b = q[r0:r0 + rows].contiguous().view(torch.uint8).reshape(-1).to(torch.int32)
+        v = torch.index_select(_PAIRS, 0, b).reshape(-1, G, 16, 2)       # unscaled values, low nibble first
+        part = (v * xg).sum((2, 3))                                        # [rows, G] group sums
+        y[r0:r0 + rows] = (part * sc[r0:r0 + rows]).sum(1)
+    return y
+
+
+def gather_m1_grouped(x, pools, inds, w):
+    """gather_m1 with every product formed by group_dot (no fp32 weight matrices)."""
+    acc = torch.zeros(pools["down_w"].shape[1], dtype=torch.float32)
+    for j in range(inds.numel()):
+        e = int(inds[j])
+        g = _bf16(group_dot(pools["gate_w"][e], pools["gate_s"][e], x))
+        u = _bf16(group_dot(pools["up_w"][e], pools["up_s"][e], x))
+        h = _bf16(_bf16(g * _bf16(torch.sigmoid(g))) * u)
+        ye = _bf16(group_dot(pools["down_w"][e], pools["down_s"][e], h))
+        acc = acc + ye * w[j]
+    return _bf16(acc)
+
+
+def decode_step(x, W, bias, pools, k=8, grouped=False):
     """One-row MoE-layer decode (router + 8 experts + combine): y fp32 [H] (bf16 values), inds, w."""
     inds, w = route(x, W, bias, k)
-    return gather_m1(x, pools, inds, w), inds, w
+    return (gather_m1_grouped if grouped else gather_m1)(x, pools, inds, w), inds, w
