@@ -28,10 +28,11 @@
  * Streams: the prefill entry points (mimo_moe_prefill, mimo_moe_prefill_staged, mimo_moe_prefill_block,
  * mimo_moe_layer_prefill) run part of each grouped GEMM on a side stream forked from and joined back to
  * `stream` with events; every (device, stream) pair has its own side stream, kept for the life of the
- * process.  A call therefore orders work only on its own `stream`: prefills on different streams never wait
- * for each other, and a prefill captured into a HIP graph captures only its own stream's work.  No entry
- * point builds anything on the device at first use (the sigmoid table is constant data), so the first call
- * of a process may itself be captured.
+ * process (the first 64 pairs; prefills on further streams run that part on `stream` itself, after the
+ * rest, with the same results).  A call therefore orders work only on its own `stream`: prefills on different
+ * streams never wait for each other, and a prefill captured into a HIP graph captures only its own stream's
+ * work.  No entry point builds anything on the device at first use (the sigmoid table is constant data), so
+ * the first call of a process may itself be captured.
  */
 #ifndef MIMO_MOE_H
 #define MIMO_MOE_H

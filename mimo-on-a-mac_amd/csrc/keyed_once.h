@@ -15,24 +15,30 @@ template <class Key, class T>
 class KeyedOnce {
  public:
   // The object of `key`, made by make() (a std::unique_ptr<T>, empty on failure) on the first request; nullptr
-  // when making it failed (a later request tries again).
+  // when making it failed (a later request tries again) or when `cap` objects exist already and `key` has none
+  // (the map never holds more than `cap` objects).
   template <class Make>
-  T* get(const Key& key, Make make) {
+  T* get(const Key& key, Make make, size_t cap = (size_t)-1) {
     std::lock_guard<std::mutex> g(mu_);
-    std::unique_ptr<T>& slot = map_[key];
-    if (!slot) slot = make();
-    return slot.get();
+    auto it = map_.find(key);
+    if (it != map_.end() && it->second) return it->second.get();
+    if (made_ >= cap) return nullptr;
+    std::unique_ptr<T> obj = make();
+    if (!obj) return nullptr;
+    T* ptr = obj.get();
+    map_[key] = std::move(obj);
+    ++made_;
+    return ptr;
   }
   size_t size() {
     std::lock_guard<std::mutex> g(mu_);
-    size_t n = 0;
-    for (auto& kv : map_) n += kv.second ? 1 : 0;
-    return n;
+    return made_;
   }
 
  private:
   std::mutex mu_;
   std::map<Key, std::unique_ptr<T>> map_;
+  size_t made_ = 0;
 };
 
 }  // namespace mimo

@@ -556,6 +556,10 @@ struct SideStream {
   hipEvent_t fork = nullptr, join = nullptr;
   std::mutex mu;
 };
+// At most kMaxSideStreams pairs get one; a prefill on any other caller stream (or one whose side stream could not
+// be created) runs both tile launches on the caller's stream, one after the other: the same results, without the
+// overlap.
+constexpr size_t kMaxSideStreams = 64;
 static SideStream* side_stream(hipStream_t caller) {
   static KeyedOnce<std::pair<int, hipStream_t>, SideStream> per;
   int dev = 0;
@@ -570,7 +574,7 @@ static SideStream* side_stream(hipStream_t caller) {
       return nullptr;
     }
     return ss;
-  });
+  }, kMaxSideStreams);
 }
 
 template <bool GATEUP, bool WIDE> static int pf_allow_lds() {
@@ -627,10 +631,11 @@ static int run_prefill(const uint16_t* x, int T, const int32_t* slot_inds, const
   using NS = PfShape<false>;
   using WS = PfShape<true>;
   SideStream* ss = tl.scap ? side_stream(st) : nullptr;
-  if (tl.scap && !ss) return set_error(MIMO_ERR_HIP, "moe prefill: cannot create the side stream");
-  // one GEMM: narrow tiles on the side stream, wide tiles on st, joined before st's next work
+  // one GEMM: narrow tiles on the side stream, wide tiles on st, joined before st's next work (without a side
+  // stream, both on st)
   auto gemm = [&](auto narrow_kernel, auto wide_kernel, int obn_narrow, int obn_wide) -> int {
     if (!ss) {
+      if (tl.scap) narrow_kernel<<<grid_of(tl.scap, obn_narrow), 512, pf_lds_bytes<false>(), st>>>(a);
       wide_kernel<<<grid_of(tl.wcap, obn_wide), 512, pf_lds_bytes<true>(), st>>>(a);
       return MIMO_OK;
     }

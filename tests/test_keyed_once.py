@@ -1,7 +1,7 @@
 """The per-(device, caller stream) side-stream map of the prefill entry points (csrc/keyed_once.h), on the CPU:
 two caller streams of one device, or one stream handle on two devices, get distinct side streams; a pair gets the
 same one on every call; a failed creation is retried; eight threads asking for the same new pair at once create
-it once.  The header is compiled with the host compiler into a small program (no HIP types in it)."""
+it once; past the cap a new pair gets none while the existing pairs keep theirs.  The header is compiled with the host compiler into a small program (no HIP types in it)."""
 import os
 import subprocess
 
@@ -49,6 +49,10 @@ int main() {
   for (auto& t : ts) t.join();
   for (int t = 1; t < 8; ++t) if (got[t] != got[0] || !got[0]) return 17;
   if (made.load() != 6) return 18;
+  // a cap: at most 7 objects; a new pair past it gets none (and is not remembered), existing pairs keep theirs
+  if (per.get(Key(3, sa), make, 7) == nullptr || per.size() != 7) return 19;
+  if (per.get(Key(4, sa), make, 7) != nullptr || per.size() != 7 || made.load() != 7) return 20;
+  if (per.get(Key(0, sa), make, 7) != a0) return 21;
   printf("ok\n");
   return 0;
 }
