@@ -17,7 +17,8 @@ hidden 256, intermediate 512):
             out exactly zero.  A second call with every weight nonzero is compared on 64 sampled tokens (16 at the
             three larger chunks); routes and samples come from a per-run seed.
   profile   2048 tokens routed with the measured per-layer popularity of MiMo layers 1 and 44
-            (tests/golden/expert_profile.npz, from the reference's engine/mimo_stream/data/expert_profile.npz).
+            (tests/golden/expert_profile.npz, from the reference's engine/mimo_stream/data/expert_profile.npz),
+            and decode of 1, 4 and 8 rows steered to experts drawn with the popularity of MiMo layers 1, 24 and 47.
   stack     48 layers (164 GB of experts resident), one decode step through every layer at 1 and 4 rows: layers
             0, 23 and 47 against the oracle, every layer bit-identical on a rerun.
 
@@ -256,6 +257,24 @@ def test_prefill_measured_popularity_every_token(stack, profile_row):
     rng = np.random.default_rng(_run_seed() + 7 * profile_row)
     inds = _profile_routes(rng, 2048, profile_row)
     _prefill_every_token(rng, stack[3], 2048, inds, f" (MiMo layer {profile_row + 1} popularity)", 64)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_decode_measured_popularity(stack, M):
+    """Decode rows steered to experts drawn with the measured popularity of MiMo layers 1, 24 and 47 (the reference's
+    expert profile; at 4-8 rows the popular experts repeat across rows, the grouping's shared-expert case): routes
+    bit-exact, y against the oracle, on three layers of the stack.  Sets and rows come from a per-run seed."""
+    import bench
+    rng = np.random.default_rng(_run_seed() + 31 * M)
+    counts = bench.profile_counts()
+    for l, prow in ((1, 0), (24, 23), (47, 46)):
+        blk = stack[l]
+        pl = counts[prow] / counts[prow].sum()
+        sets = [list(rng.choice(E, K, replace=False, p=pl)) for _ in range(M)]
+        W = blk.router.weight.float().cpu().numpy()
+        x = oq.round_bf16(bench.steered_rows(rng, W, sets))
+        _check_decode(blk, x, f"decode {M} rows, MiMo layer {prow + 1} popularity, layer {l}", layer=l,
+                      distinct=int(len(np.unique(np.concatenate(sets)))))
 
 
 @pytest.mark.parametrize("M", [1, 4])
