@@ -344,8 +344,9 @@ def stack_case(layers, M, tokens, device, seed, popularity="zipf"):
 HEADLINE_KERNEL = ("decode_gateup_kernel<8, true, false, true>", 32768, 8)   # 1-row decode: 128 x 8 blocks of 256
 
 
-def trace_parse(d):
-    """rocprofv3 kernel trace of bench.py -> markdown on stdout, headline figures to profiles/trace.json."""
+def trace_parse(d, out_path=None):
+    """rocprofv3 kernel trace of bench.py -> markdown on stdout, headline figures to profiles/trace.json (or
+    out_path)."""
     import collections
     import csv
     rows = []
@@ -383,7 +384,7 @@ def trace_parse(d):
               f"average interval from the previous kernel's end on its queue to its own end "
               f"{out['decode_gateup_kernel:decode_m1']['after_previous_end_us']:.2f} µs (the interval the "
               f"benchmark's chained HIP events measure).")
-        with open(os.path.join(ROOT, "profiles", "trace.json"), "w") as f:
+        with open(out_path or os.path.join(ROOT, "profiles", "trace.json"), "w") as f:
             json.dump(out, f, indent=1)
 
 
