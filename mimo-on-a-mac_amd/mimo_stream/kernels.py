@@ -38,6 +38,11 @@ def group_routes(inds, scores, R=8, slot_of=None, n_slots=None, device="cuda"):
     scores_d = _dev(scores, torch.float32, device)
     M, k = inds_d.shape
     so = None if slot_of is None else _dev(slot_of, torch.int32, device)
+    if M * k == 0:                          # no routes: no distinct experts (np.unique of nothing), no launch
+        dev = inds_d.device
+        return (torch.empty(0, dtype=torch.int32, device=dev), torch.empty((0, R), dtype=torch.int32, device=dev),
+                torch.empty(0, dtype=torch.int32, device=dev), torch.empty((0, R), dtype=torch.float32, device=dev),
+                torch.empty(0, dtype=torch.int32, device=dev))
     if n_slots is None:
         n_slots = int(so.max().item()) + 1 if so is not None else int(inds_d.max().item()) + 1
     Umax = min(M * k, n_slots)
@@ -89,6 +94,13 @@ def moe_experts(x, pools, uslot, urows, ucnt, uw, R=8, gather_idx=None, round_ex
     dev = x.device
     x = x.to(torch.bfloat16).contiguous()
     M = x.shape[0]
+    if M == 0:                              # no rows: an empty output, no launch
+        bank = bank_struct(pools)
+        y = torch.empty((0, bank.hidden), dtype=torch.bfloat16, device=dev)
+        if return_intermediates:
+            return (y, torch.empty((0, R, bank.inter), dtype=torch.bfloat16, device=dev),
+                    torch.empty((0, R, bank.hidden), dtype=torch.float32, device=dev))
+        return y
     uslot, urows, ucnt = (_dev(a, torch.int32, dev) for a in (uslot, urows, ucnt))
     uw = _dev(uw, torch.float32, dev)
     Umax = uslot.shape[0]

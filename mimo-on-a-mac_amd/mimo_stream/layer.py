@@ -50,6 +50,8 @@ class MoELayer:
         """post_attention_layernorm(x): bf16 [T, H] (model.py:299)."""
         x2 = self._rows(x)
         r = torch.empty_like(x2)
+        if x2.shape[0] == 0:
+            return r
         _lib.call("mimo_rmsnorm", _lib.ptr(x2), x2.shape[0], self.hidden, _lib.ptr(self.norm_weight), self.eps,
                   _lib.ptr(r), _lib.stream_ptr(x2.device))
         return r
@@ -66,6 +68,15 @@ class MoELayer:
         x2 = self._rows(x)
         T = x2.shape[0]
         dev = x2.device
+        if T == 0:                          # an empty batch: h = x, nothing routed, no launch
+            k = self._inner.router.top_k
+            out = (x2.clone().reshape(x.shape),)
+            if return_routes:
+                out += (torch.empty((0, k), dtype=torch.int32, device=dev),
+                        torch.empty((0, k), dtype=torch.float32, device=dev))
+            if return_norm:
+                out += (torch.empty_like(x2),)
+            return out if len(out) > 1 else out[0]
         if isinstance(self.block, StreamedMoEBlock) or self._inner.router.gate_options is not None:
             r = self.norm(x2)
             y, inds, w = self.block(r, return_routes=True)

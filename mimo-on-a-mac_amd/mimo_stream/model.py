@@ -48,6 +48,8 @@ class Router:
         logits = torch.empty((T, En), dtype=torch.float32, device=dev)
         inds = torch.empty((T, self.top_k), dtype=torch.int32, device=dev)
         w = torch.empty((T, self.top_k), dtype=torch.float32, device=dev)
+        if T == 0:                          # an empty batch routes nothing (no launch)
+            return logits, inds, w
         _lib.call("mimo_router", _lib.ptr(r2), _lib.ptr(self.weight.contiguous()),
                   _lib.ptr(self.e_score_correction_bias.contiguous()), T, H, En, self.top_k, _lib.ptr(logits),
                   _lib.ptr(inds), _lib.ptr(w), _lib.stream_ptr(dev))
@@ -139,6 +141,8 @@ class MoEBlock:
         if T > VERIFY_MAX:
             raise ValueError(f"_moe_small takes at most {VERIFY_MAX} rows")
         dev = r2.device
+        if T == 0:
+            return torch.empty((0, self._bank_struct.hidden), dtype=torch.bfloat16, device=dev)
         S = self.n_slots
         slot_inds = self._slots(inds)
         w = w.to(torch.float32).contiguous()
@@ -171,6 +175,8 @@ class MoEBlock:
         _lib.require_cuda(r2)
         T, k = inds.shape
         dev = r2.device
+        if T == 0:
+            return torch.empty((0, self._bank_struct.hidden), dtype=torch.bfloat16, device=dev)
         x = r2.to(torch.bfloat16).contiguous()
         slot_inds = self._slots(inds)
         w = w.to(torch.float32).contiguous()
@@ -202,6 +208,8 @@ class MoEBlock:
         y = torch.empty((T, b.hidden), dtype=torch.bfloat16, device=dev)
         inds = torch.empty((T, k), dtype=torch.int32, device=dev)
         w = torch.empty((T, k), dtype=torch.float32, device=dev)
+        if T == 0:                          # an empty batch: empty outputs, no launch
+            return (y, inds, w) if return_routes else y
         st = _lib.stream_ptr(dev)
         args = (_lib.ptr(r2), T, _lib.ptr(rt.weight), _lib.ptr(rt.e_score_correction_bias), _lib.ptr(self.slot_of), En, k,
                 b, _lib.ptr(y), _lib.ptr(inds), _lib.ptr(w), _lib.ptr(self.status))

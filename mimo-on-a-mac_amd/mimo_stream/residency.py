@@ -166,6 +166,8 @@ class StreamedMoEBlock:
     def __call__(self, r, return_routes=False):
         r2 = r.reshape(-1, r.shape[-1]).to(torch.bfloat16).contiguous()
         T = r2.shape[0]
+        if T == 0:                          # an empty batch: nothing to route or load
+            return self.block(r2, return_routes=return_routes)
         inds, w = self.block.router(r2)
         inds_h = inds.cpu().numpy()               # the host needs the routes to decide what to load
         if T <= pools.VERIFY_MAX:
