@@ -5,7 +5,7 @@ hidden 256, intermediate 512):
   tiny      the plumbing layer, decode (4 rows) and prefill (32 tokens), every element compared.
   1 row     one MoE layer, all 256 experts resident, decode of single rows (the M = 1 path, model.py:173-182):
             routes bit-exact given the logits, y against the oracle on a sub-pool of the selected experts.
-  rows      the same layer at 2, 4 and 8 rows with routing steered so consecutive rows share experts (the
+  rows      the same layer at 2 to 8 rows with routing steered so consecutive rows share experts (the
             distinct-expert kernels, kernels.py:176-199).
   prefill   Zipf(1.1) routes at 512, 2048, 4096, 5001 and 6250 tokens (4096 = the reference server's chunk,
             engine/server.py:34: 32,768 slot-sorted routes; 40,008 and 50,000 routes past 32,767 and off multiples
@@ -161,7 +161,7 @@ def test_decode_one_row_256_experts(rng, stack):
         _check_decode(blk, x, f"decode 1 row, 256 experts, step {step}")
 
 
-@pytest.mark.parametrize("M", [2, 4, 8])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 6, 7, 8])
 def test_decode_rows_256_experts(rng, stack, M):
     _check_decode(stack[1], _steered(rng, stack[1], M), f"decode {M} rows, 256 experts")
 
